@@ -1,0 +1,101 @@
+"""ctypes binding of libalgx.so (the C ABI declared in include/algx.h).
+
+The library is built in-tree by ``algebraic-extra_amd/build.py`` (or
+``__graft_entry__.build()``). There is no fallback: every operator of this
+package calls into the HIP library and raises if it is missing.
+"""
+
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libalgx.so")
+
+BF16, F32 = 0, 1
+SOFTMAX, ASINH = 0, 1
+HEAD_CE, HEAD_ALG_CE = 0, 1
+
+_i32, _i64, _f32, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+
+
+class AttnVariant(ctypes.Structure):
+    """algx_attn_variant (include/algx.h)."""
+    _fields_ = [("kind", _i32), ("n", _i32), ("shift", _i32), ("fast_rho", _i32),
+                ("inv_stat", _i32), ("bounded_scores", _i32), ("precise_output", _i32),
+                ("clamp", _f32)]
+
+
+_VP = ctypes.POINTER(AttnVariant)
+
+# name -> (restype, argtypes); must match include/algx.h.
+SIGNATURES = {
+    "algx_last_error": (ctypes.c_char_p, []),
+    "algx_version": (_i32, []),
+    "algx_selftest_mfma32": (_i32, [_p, _p, _p, _p]),
+    "algx_qknorm_fwd": (_i32, [_p, _p, _p, _i64, _i32, _i32, _f32, _p]),
+    "algx_qknorm_bwd_workspace_bytes": (_i64, [_i64, _i32, _i32]),
+    "algx_qknorm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _f32, _p]),
+    "algx_attn_guard_words": (_i32, []),
+    "algx_attn_guard": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _f32,
+                               _f32, _p]),
+    "algx_attn_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32,
+                             _VP, _VP, _p, _p]),
+    "algx_attn_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
+    "algx_attn_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,
+                             _i32, _i32, _i32, _f32, _VP, _VP, _p, _p]),
+    "algx_head_fwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
+    "algx_head_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _f32,
+                             _i32, _p]),
+    "algx_head_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
+    "algx_head_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32,
+                             _f32, _f32, _i32, _p]),
+}
+
+_lib = None
+
+
+def load():
+    """Load libalgx.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with "
+                               "`python algebraic-extra_amd/build.py`")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def call(name, *args):
+    """Call a status-returning entry point; raise RuntimeError on failure."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.algx_last_error().decode()
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def query(name, *args):
+    return getattr(load(), name)(*args)
+
+
+def ptr(t):
+    """Device pointer of a tensor (or None)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def dtype_code(dtype):
+    import torch
+    if dtype == torch.bfloat16:
+        return BF16
+    if dtype == torch.float32:
+        return F32
+    raise ValueError(f"unsupported dtype {dtype}")

@@ -1,0 +1,5 @@
+"""Reference-compatible operators: flash_attention, fused_head, qk_rms_norm."""
+
+from .flash import Variant, flash_attention, make_variant  # noqa: F401
+from .fused_head import fused_head  # noqa: F401
+from .qk_norm import qk_rms_norm  # noqa: F401

@@ -1,0 +1,143 @@
+// C ABI of the attention kernels: argument validation, variant conversion
+// and dispatch between the MFMA path (bf16, D=64, T%128==0) and the generic
+// path (everything else). Guarded calls enqueue both variants; each kernel
+// reads the device guard word and returns at once when it is not selected,
+// mirroring lax.cond(in_range, low, high) of flash.py:853-856 without a host
+// round trip.
+#include <cstdlib>
+
+#include "attn_aux.h"
+
+namespace algx {
+namespace {
+
+int32_t to_kvar(const algx_attn_variant* v, KVariant& out, const char* which) {
+  if (v == nullptr) return fail(std::string("attn: missing ") + which + " variant");
+  if (v->kind != ALGX_SOFTMAX && v->kind != ALGX_ASINH)
+    return fail(std::string("attn: unknown kind in ") + which + " variant");
+  if (v->kind == ALGX_ASINH && (v->n < 2 || (v->n & (v->n - 1))))
+    return fail("attn: asinh kernel needs n to be a power of two");
+  if (v->kind == ALGX_ASINH && v->inv_stat && v->shift)
+    return fail("attn: inverse-denominator statistic requires shift=False");
+  out.kind = v->kind;
+  out.log2n = v->kind == ALGX_ASINH ? ilog2(v->n) : 0;
+  out.shift = v->kind == ALGX_SOFTMAX ? 1 : (v->shift != 0);
+  out.fast = v->fast_rho != 0;
+  out.inv_stat = v->inv_stat != 0;
+  out.bounded = v->bounded_scores != 0;
+  out.precise = v->precise_output != 0;
+  out.clamp = v->clamp;
+  out.slope = v->kind == ALGX_ASINH ? (float)v->n : 1.0f;
+  return 0;
+}
+
+bool force_generic() {
+  const char* e = std::getenv("ALGX_FORCE_GENERIC");
+  return e != nullptr && e[0] == '1';
+}
+
+int32_t check_shape(int B, int H, int T, int D, int dtype) {
+  if (B < 0 || H < 0 || T < 0) return fail("attn: negative size");
+  if (dtype != ALGX_BF16 && dtype != ALGX_F32) return fail("attn: dtype must be bf16 or f32");
+  if (D != 16 && D != 32 && D != 64) return fail("attn: head dim must be 16, 32 or 64");
+  return 0;
+}
+
+}  // namespace
+}  // namespace algx
+
+using namespace algx;
+
+extern "C" int32_t algx_attn_guard_words(void) { return guard_words(); }
+
+extern "C" int32_t algx_attn_guard(const void* q, const void* k, const void* v, const float* sink,
+                                   int32_t* guard, int32_t B, int32_t H, int32_t T, int32_t D,
+                                   int32_t dtype, float q_scale, float bound, float vmax,
+                                   void* stream) {
+  if (int32_t rc = check_shape(B, H, T, D, dtype)) return rc;
+  if (guard == nullptr) return fail("attn_guard: null guard buffer");
+  if ((int64_t)B * H * T > 0 && (q == nullptr || k == nullptr || v == nullptr))
+    return fail("attn_guard: null input");
+  return launch_guard(q, k, v, sink, guard, B, H, T, D, dtype, q_scale, bound, vmax,
+                      (hipStream_t)stream);
+}
+
+extern "C" int32_t algx_attn_fwd(const void* q, const void* k, const void* v, const float* sink,
+                                 void* o, float* o_precise, float* stat, int32_t B, int32_t H,
+                                 int32_t T, int32_t D, int32_t dtype, float q_scale,
+                                 const algx_attn_variant* low, const algx_attn_variant* high,
+                                 const int32_t* guard, void* stream) {
+  if (int32_t rc = check_shape(B, H, T, D, dtype)) return rc;
+  KVariant kl{}, kh{};
+  if (int32_t rc = to_kvar(low, kl, "low")) return rc;
+  if (guard != nullptr)
+    if (int32_t rc = to_kvar(high, kh, "high")) return rc;
+  if ((int64_t)B * H * T == 0) return 0;
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || stat == nullptr)
+    return fail("attn_fwd: null pointer");
+  if ((kl.precise || (guard != nullptr && kh.precise)) && o_precise == nullptr)
+    return fail("attn_fwd: precise-output variant needs o_precise");
+  hipStream_t s = (hipStream_t)stream;
+  const bool mfma = mfma_supported(T, D, dtype) && !force_generic();
+  auto run = [&](const KVariant& var, int want_low) -> int32_t {
+    return mfma ? launch_fwd_mfma(q, k, v, sink, o, o_precise, stat, B, H, T, q_scale, var,
+                                  guard, want_low, s)
+                : launch_fwd_generic(q, k, v, sink, o, o_precise, stat, B, H, T, D, dtype,
+                                     q_scale, var, guard, want_low, s);
+  };
+  if (int32_t rc = run(kl, 1)) return rc;
+  if (guard != nullptr) return run(kh, 0);
+  return 0;
+}
+
+extern "C" int64_t algx_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t T, int32_t D) {
+  const int64_t rows = (int64_t)B * H * T;
+  const int64_t acc = rows * D * (int64_t)sizeof(float);
+  const int64_t di = ((rows * (int64_t)sizeof(float) + 255) / 256) * 256;
+  return acc + di;
+}
+
+extern "C" int32_t algx_attn_bwd(const void* q, const void* k, const void* v, const float* sink,
+                                 const void* o, const float* o_precise, const float* stat,
+                                 const void* dout, void* dq, void* dk, void* dv, float* dsink,
+                                 void* workspace, int32_t B, int32_t H, int32_t T, int32_t D,
+                                 int32_t dtype, float q_scale, const algx_attn_variant* low,
+                                 const algx_attn_variant* high, const int32_t* guard,
+                                 void* stream) {
+  if (int32_t rc = check_shape(B, H, T, D, dtype)) return rc;
+  KVariant kl{}, kh{};
+  if (int32_t rc = to_kvar(low, kl, "low")) return rc;
+  if (guard != nullptr) {
+    if (int32_t rc = to_kvar(high, kh, "high")) return rc;
+  } else {
+    kh = kl;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t rows = (int64_t)B * H * T;
+  if (rows == 0) {
+    if (sink != nullptr && dsink != nullptr) return fill_f32(dsink, H, 0.0f, s);
+    return 0;
+  }
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || stat == nullptr ||
+      dout == nullptr || dq == nullptr || dk == nullptr || dv == nullptr || workspace == nullptr)
+    return fail("attn_bwd: null pointer");
+  if ((kl.precise || kh.precise) && o_precise == nullptr)
+    return fail("attn_bwd: precise-output variant needs o_precise");
+  const bool mfma = mfma_supported(T, D, dtype) && !force_generic();
+  float* dq_acc = (float*)workspace;
+  float* di = (float*)((char*)workspace + rows * D * (int64_t)sizeof(float));
+  if (int32_t rc = launch_bwd_pre(dout, o, o_precise, stat, sink, di, mfma ? dq_acc : nullptr,
+                                  dsink, B, H, T, D, dtype, kl, kh, guard, s))
+    return rc;
+  auto run = [&](const KVariant& var, int want_low) -> int32_t {
+    return mfma ? launch_bwd_mfma(q, k, v, stat, di, dout, dq_acc, dk, dv, B, H, T, q_scale, var,
+                                  guard, want_low, s)
+                : launch_bwd_generic(q, k, v, stat, di, dout, dq, dk, dv, B, H, T, D, dtype,
+                                     q_scale, var, guard, want_low, s);
+  };
+  if (int32_t rc = run(kl, 1)) return rc;
+  if (guard != nullptr)
+    if (int32_t rc = run(kh, 0)) return rc;
+  if (mfma) return launch_dq_finish(dq_acc, dq, rows * D, dtype, kl, kh, guard, q_scale, s);
+  return 0;
+}

@@ -1,0 +1,495 @@
+// Fused tied-embedding projection + likelihood loss (fused_head.py) on gfx950.
+//
+// Forward (fused_head.py:72-117, :174-191): logits z^T = E h^T are formed
+// tile by tile (128 vocab x 128 tokens, d streamed through LDS in 64-wide
+// stages, v_mfma_f32_32x32x16_bf16) and never stored. Vocabulary rows sit on
+// the MFMA M axis so every lane holds 16 vocabulary values of one token; the
+// per-token statistic (online max/sum-exp for "ce", sum of rho(min(z/c,X))^n
+// for "alg_ce") is kept per lane, merged across lanes at the end of a
+// workgroup's vocabulary chunk, and merged across chunks by a small kernel.
+// The target logit is written by the one lane that meets it.
+//
+// Backward (fused_head.py:120-156, :194-216): the same tiles are recomputed
+// and the scaled bf16 logit gradient dz (fused_head.py:145) is written for a
+// chunk of tokens; dh = dz E and dE += dz^T h are then plain MFMA GEMMs over
+// that chunk (the reference also materialises dz and runs an XLA GEMM for dE).
+#include "common.h"
+
+namespace algx {
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int LSTR = BK + 8;  // LDS row stride (bf16): 144 B
+constexpr int kThreads = 256;
+constexpr int kVocabChunkTiles = 16;  // vocabulary tiles per forward workgroup
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Operand of a GEMM C[m][n] = sum_k A(m,k) B(n,k). KC: stored as [MN][K]
+// (k contiguous, leading dimension ld); otherwise stored as [K][MN].
+struct Operand {
+  const bf16* p;
+  int64_t ld;
+  int rows;  // extent along m (or n)
+  int K;
+};
+
+// Stages one BM x BK tile of an operand into registers (zero outside).
+template <bool KC>
+struct TileLoader {
+  bf16x8 r[4];
+  __device__ __forceinline__ void load(const Operand& op, int mn0, int k0, int tid) {
+    if (KC) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int id = tid + kThreads * c;
+        const int row = mn0 + (id >> 3), col = k0 + (id & 7) * 8;
+        if (row < op.rows && col < op.K)
+          r[c] = *reinterpret_cast<const bf16x8*>(op.p + (int64_t)row * op.ld + col);
+        else
+          r[c] = bf16x8{};
+      }
+    } else {
+      // 4 consecutive k rows x 8 consecutive m: unit = (k group kg, m group mg).
+      const int kg = tid >> 4, mg = tid & 15;
+      const int mm = mn0 + 8 * mg;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kk = k0 + 4 * kg + i;
+        if (kk < op.K && mm < op.rows)
+          r[i] = *reinterpret_cast<const bf16x8*>(op.p + (int64_t)kk * op.ld + mm);
+        else
+          r[i] = bf16x8{};
+      }
+    }
+  }
+  __device__ __forceinline__ void store(bf16* lds, int tid) const {
+    if (KC) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int id = tid + kThreads * c;
+        *reinterpret_cast<bf16x8*>(lds + (id >> 3) * LSTR + (id & 7) * 8) = r[c];
+      }
+    } else {
+      const int kg = tid >> 4, mg = tid & 15;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        bf16x4 col = {r[0][e], r[1][e], r[2][e], r[3][e]};
+        *reinterpret_cast<bf16x4*>(lds + (8 * mg + e) * LSTR + 4 * kg) = col;
+      }
+    }
+  }
+};
+
+// acc[i][j][r] = C[m0 + 64wm + 32i + 8(r/4) + 4g + r%4][n0 + 64wn + 32j + c32]
+struct Acc {
+  f32x16 v[2][2];
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[i][j][r] = 0.0f;
+  }
+};
+
+__device__ __forceinline__ void mma_stage(const bf16* As, const bf16* Bs, Acc& acc, int wm,
+                                          int wn, int g, int c32) {
+#pragma unroll
+  for (int ks = 0; ks < BK / 16; ++ks) {
+    bf16x8 a[2], b[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      a[i] = *reinterpret_cast<const bf16x8*>(As + (64 * wm + 32 * i + c32) * LSTR + 16 * ks + 8 * g);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      b[j] = *reinterpret_cast<const bf16x8*>(Bs + (64 * wn + 32 * j + c32) * LSTR + 16 * ks + 8 * g);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc.v[i][j] = mfma32(a[i], b[j], acc.v[i][j]);
+  }
+}
+
+// Full-K product of one output tile with a double-buffered LDS pipeline.
+template <bool AKC, bool BKC>
+__device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int m0, int n0,
+                                          bf16* As, bf16* Bs, Acc& acc, int tid) {
+  const int w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
+  const int wm = w >> 1, wn = w & 1;
+  const int K = A.K;
+  const int nk = (K + BK - 1) / BK;
+  TileLoader<AKC> la;
+  TileLoader<BKC> lb;
+  acc.zero();
+  la.load(A, m0, 0, tid);
+  lb.load(B, n0, 0, tid);
+  __syncthreads();  // previous users of the LDS buffers are done
+  la.store(As, tid);
+  lb.store(Bs, tid);
+  __syncthreads();
+  for (int kk = 0; kk < nk; ++kk) {
+    const int buf = kk & 1;
+    if (kk + 1 < nk) {
+      la.load(A, m0, (kk + 1) * BK, tid);
+      lb.load(B, n0, (kk + 1) * BK, tid);
+    }
+    mma_stage(As + buf * BM * LSTR, Bs + buf * BN * LSTR, acc, wm, wn, g, c32);
+    if (kk + 1 < nk) {
+      la.store(As + (buf ^ 1) * BM * LSTR, tid);
+      lb.store(Bs + (buf ^ 1) * BN * LSTR, tid);
+    }
+    __syncthreads();
+  }
+}
+
+// alg_ce weight w = (x + sqrt(1+x^2))^n with x = min(z/c, clamp) (fused_head.py:98-100).
+__device__ __forceinline__ float alg_weight(float z, float inv_c, float clamp, int log2n,
+                                            float& r) {
+  const float x = __builtin_fminf(z * inv_c, clamp);
+  return pow2n(rho_fast(x, r), log2n);
+}
+
+// Forward statistics. grid = (token blocks) x (vocabulary chunks).
+// partial[(chunk * N + token) * 2 + {0,1}] = (m, l) for ce, (-, l) for alg_ce.
+template <int KIND>
+__global__ __launch_bounds__(kThreads) void head_fwd_kernel(
+    const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
+    float* __restrict__ zt, float* __restrict__ partial, int N, int d, int V, int log2n,
+    float inv_c, float clamp) {
+  __shared__ __attribute__((aligned(16))) bf16 As[2 * BM * LSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * BN * LSTR];
+  __shared__ float red_m[4][BN], red_l[4][BN];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
+  const int wm = w >> 1, wn = w & 1;
+  const int n0 = blockIdx.x * BN;
+  const int chunk = blockIdx.y;
+  const int ntiles_v = (V + BM - 1) / BM;
+  const int t_begin = chunk * kVocabChunkTiles;
+  const int t_end = min(ntiles_v, t_begin + kVocabChunkTiles);
+  const Operand A{e, d, V, d};
+  const Operand B{h, d, N, d};
+  int tok[2], tgt[2];
+  float m_st[2], l_st[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    tok[j] = n0 + 64 * wn + 32 * j + c32;
+    tgt[j] = tok[j] < N ? targets[tok[j]] : -1;
+    m_st[j] = -1e30f;
+    l_st[j] = 0.0f;
+  }
+  Acc acc;
+  for (int t = t_begin; t < t_end; ++t) {
+    const int m0 = t * BM;
+    gemm_tile<true, true>(A, B, m0, n0, As, Bs, acc, tid);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float tile_max = -1e30f;
+      if (KIND == ALGX_HEAD_CE) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (m < V) tile_max = __builtin_fmaxf(tile_max, acc.v[i][j][r]);
+          }
+      }
+      const float m_new = __builtin_fmaxf(m_st[j], tile_max);
+      float lsum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+          const float z = acc.v[i][j][r];
+          if (m == tgt[j]) zt[tok[j]] = z;
+          float wgt;
+          if (KIND == ALGX_HEAD_CE) {
+            wgt = __builtin_amdgcn_exp2f((z - m_new) * 1.4426950408889634f);
+          } else {
+            float rr;
+            wgt = alg_weight(z, inv_c, clamp, log2n, rr);
+          }
+          lsum += m < V ? wgt : 0.0f;
+        }
+      if (KIND == ALGX_HEAD_CE) {
+        l_st[j] = l_st[j] * __builtin_amdgcn_exp2f((m_st[j] - m_new) * 1.4426950408889634f) + lsum;
+        m_st[j] = m_new;
+      } else {
+        l_st[j] += lsum;
+      }
+    }
+  }
+  // Merge the 4 partial states of each token: lane halves g and waves wm.
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    float mo = __shfl_xor(m_st[j], 32, 64), lo = __shfl_xor(l_st[j], 32, 64);
+    if (KIND == ALGX_HEAD_CE) {
+      const float mm = __builtin_fmaxf(m_st[j], mo);
+      l_st[j] = l_st[j] * __builtin_amdgcn_exp2f((m_st[j] - mm) * 1.4426950408889634f) +
+                lo * __builtin_amdgcn_exp2f((mo - mm) * 1.4426950408889634f);
+      m_st[j] = mm;
+    } else {
+      l_st[j] += lo;
+    }
+    if (g == 0) {
+      red_m[wm * 2 + j][64 * wn + c32] = m_st[j];
+      red_l[wm * 2 + j][64 * wn + c32] = l_st[j];
+    }
+  }
+  __syncthreads();
+  if (tid < BN) {
+    const int col = tid, jj = (col & 63) >> 5;  // column -> (wn, j, c32)
+    const int wnn = col >> 6, cc = col & 31;
+    const int slot = 64 * wnn + cc;
+    const float m_a = red_m[0 * 2 + jj][slot], l_a = red_l[0 * 2 + jj][slot];
+    const float m_b = red_m[1 * 2 + jj][slot], l_b = red_l[1 * 2 + jj][slot];
+    float m_out, l_out;
+    if (KIND == ALGX_HEAD_CE) {
+      m_out = __builtin_fmaxf(m_a, m_b);
+      l_out = l_a * __builtin_amdgcn_exp2f((m_a - m_out) * 1.4426950408889634f) +
+              l_b * __builtin_amdgcn_exp2f((m_b - m_out) * 1.4426950408889634f);
+    } else {
+      m_out = 0.0f;
+      l_out = l_a + l_b;
+    }
+    const int token = n0 + col;
+    if (token < N) {
+      partial[((int64_t)chunk * N + token) * 2 + 0] = m_out;
+      partial[((int64_t)chunk * N + token) * 2 + 1] = l_out;
+    }
+  }
+}
+
+// stat = m + log l (ce) or l^(-1/n) (alg_ce) from the chunk partials
+// (fused_head.py:113-116).
+template <int KIND>
+__global__ __launch_bounds__(256) void head_stat_kernel(const float* __restrict__ partial,
+                                                        int nchunks, int N, int log2n,
+                                                        float* __restrict__ stat) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= N) return;
+  float m = -1e30f, l = 0.0f;
+  for (int c = 0; c < nchunks; ++c) {
+    const float mc = partial[((int64_t)c * N + t) * 2 + 0];
+    const float lc = partial[((int64_t)c * N + t) * 2 + 1];
+    if (KIND == ALGX_HEAD_CE) {
+      const float mm = __builtin_fmaxf(m, mc);
+      l = l * __expf(m - mm) + lc * __expf(mc - mm);
+      m = mm;
+    } else {
+      l += lc;
+    }
+  }
+  stat[t] = KIND == ALGX_HEAD_CE ? m + __logf(l) : inv_root(l, log2n);
+}
+
+// dz tile of a token chunk: dz[t][v] = bf16(f(z) * scale), 0 for padded v.
+template <int KIND>
+__global__ __launch_bounds__(kThreads) void head_dz_kernel(
+    const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
+    const float* __restrict__ stat, const float* __restrict__ scale, bf16* __restrict__ dz,
+    int64_t ldz, int tok0, int ntok, int d, int V, int log2n, float inv_c, float clamp) {
+  __shared__ __attribute__((aligned(16))) bf16 As[2 * BM * LSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * BN * LSTR];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
+  const int wm = w >> 1, wn = w & 1;
+  const int n0 = blockIdx.x * BN;   // token offset inside the chunk
+  const int m0 = blockIdx.y * BM;   // vocabulary offset
+  const Operand A{e, d, V, d};
+  const Operand B{h + (int64_t)tok0 * d, d, ntok, d};
+  Acc acc;
+  gemm_tile<true, true>(A, B, m0, n0, As, Bs, acc, tid);
+  const float sc = scale[0];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int tl = n0 + 64 * wn + 32 * j + c32;
+    if (tl >= ntok) continue;
+    const int tgt = targets[tok0 + tl];
+    const float st = stat[tok0 + tl];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int mb = m0 + 64 * wm + 32 * i + 8 * q4 + 4 * g;
+        bf16x4 out;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int m = mb + u;
+          const float z = acc.v[i][j][4 * q4 + u];
+          const float y = m == tgt ? 1.0f : 0.0f;
+          float g_z;
+          if (KIND == ALGX_HEAD_CE) {
+            g_z = __builtin_amdgcn_exp2f((z - st) * 1.4426950408889634f) - y;
+          } else {
+            const float x = __builtin_fminf(z * inv_c, clamp);
+            float r;
+            const float p = pow2n(rho_fast(x, r) * st, log2n);
+            g_z = (p - y) * r;
+          }
+          out[u] = (bf16)(m < V ? g_z * sc : 0.0f);
+        }
+        *reinterpret_cast<bf16x4*>(dz + (int64_t)tl * ldz + mb) = out;
+      }
+  }
+}
+
+// Plain GEMM C[m][n] (+)= sum_k A(m,k) B(n,k) with float32 or bf16 output.
+template <bool AKC, bool BKC, typename TOut, bool ACCUM>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(Operand A, Operand B, TOut* __restrict__ C,
+                                                        int64_t ldc, int M, int N) {
+  __shared__ __attribute__((aligned(16))) bf16 As[2 * BM * LSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * BN * LSTR];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
+  const int wm = w >> 1, wn = w & 1;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  Acc acc;
+  gemm_tile<AKC, BKC>(A, B, m0, n0, As, Bs, acc, tid);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 64 * wn + 32 * j + c32;
+      if (n >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (m >= M) continue;
+        TOut* dst = C + (int64_t)m * ldc + n;
+        if (ACCUM)
+          *dst = from_f<TOut>(to_f(*dst) + acc.v[i][j][r]);
+        else
+          *dst = from_f<TOut>(acc.v[i][j][r]);
+      }
+    }
+}
+
+int64_t vpad_of(int V) { return ((int64_t)V + BM - 1) / BM * BM; }
+
+// Token chunk of the backward: bounds the dz scratch to ~1 GiB.
+int chunk_tokens(int N, int V) {
+  const int64_t per_tok = vpad_of(V) * 2;
+  int64_t c = ((int64_t)1 << 30) / per_tok;
+  c = c / BN * BN;
+  if (c < BN) c = BN;
+  return (int)(c > N ? ((N + BN - 1) / BN) * BN : c);
+}
+
+int32_t check_head(const void* h, const void* E, const int32_t* targets, int N, int d, int V,
+                   int kind, int n, int dtype) {
+  if (N < 0 || d <= 0 || V <= 0) return fail("head: invalid sizes");
+  if (dtype != ALGX_BF16) return fail("head: the MFMA head takes bfloat16 hidden states");
+  if (d % 8) return fail("head: hidden width must be a multiple of 8");
+  if (kind != ALGX_HEAD_CE && kind != ALGX_HEAD_ALG_CE) return fail("head: unknown kind");
+  if (kind == ALGX_HEAD_ALG_CE && (n < 1 || (n & (n - 1)))) return fail("head: n must be a power of two");
+  if (N > 0 && (h == nullptr || E == nullptr || targets == nullptr)) return fail("head: null input");
+  return 0;
+}
+
+int nchunks_of(int V) {
+  const int nt = (V + BM - 1) / BM;
+  return (nt + kVocabChunkTiles - 1) / kVocabChunkTiles;
+}
+
+}  // namespace
+}  // namespace algx
+
+using namespace algx;
+
+extern "C" int64_t algx_head_fwd_workspace_bytes(int32_t N, int32_t d, int32_t V, int32_t dtype) {
+  (void)d;
+  (void)dtype;
+  return (int64_t)nchunks_of(V) * N * 2 * sizeof(float);
+}
+
+extern "C" int32_t algx_head_fwd(const void* h, const void* E, const int32_t* targets,
+                                 float* stat, float* zt, void* workspace, int32_t N, int32_t d,
+                                 int32_t V, int32_t kind, int32_t n, float inv_c, float clamp,
+                                 int32_t dtype, void* stream) {
+  if (int32_t rc = check_head(h, E, targets, N, d, V, kind, n, dtype)) return rc;
+  if (N == 0) return 0;
+  if (stat == nullptr || zt == nullptr || workspace == nullptr) return fail("head_fwd: null output");
+  hipStream_t s = (hipStream_t)stream;
+  const int nch = nchunks_of(V);
+  dim3 grid((N + BN - 1) / BN, nch);
+  const int log2n = kind == ALGX_HEAD_ALG_CE ? ilog2(n) : 0;
+  float* partial = (float*)workspace;
+  // The target logit starts at 0 as in fused_head.py:80 (a target outside
+  // the vocabulary tiles is never met).
+  if (int32_t rc = fill_f32(zt, N, 0.0f, s)) return rc;
+  if (kind == ALGX_HEAD_CE)
+    head_fwd_kernel<ALGX_HEAD_CE><<<grid, kThreads, 0, s>>>(
+        (const bf16*)h, (const bf16*)E, targets, zt, partial, N, d, V, log2n, inv_c, clamp);
+  else
+    head_fwd_kernel<ALGX_HEAD_ALG_CE><<<grid, kThreads, 0, s>>>(
+        (const bf16*)h, (const bf16*)E, targets, zt, partial, N, d, V, log2n, inv_c, clamp);
+  if (int32_t rc = check_launch("head_fwd")) return rc;
+  const int nb = (N + 255) / 256;
+  if (kind == ALGX_HEAD_CE)
+    head_stat_kernel<ALGX_HEAD_CE><<<nb, 256, 0, s>>>(partial, nch, N, log2n, stat);
+  else
+    head_stat_kernel<ALGX_HEAD_ALG_CE><<<nb, 256, 0, s>>>(partial, nch, N, log2n, stat);
+  return check_launch("head_stat");
+}
+
+extern "C" int64_t algx_head_bwd_workspace_bytes(int32_t N, int32_t d, int32_t V, int32_t dtype) {
+  (void)d;
+  (void)dtype;
+  if (N <= 0) return 0;
+  return (int64_t)chunk_tokens(N, V) * vpad_of(V) * 2;
+}
+
+extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* targets,
+                                 const float* stat, const float* scale, void* dh, float* dE,
+                                 void* workspace, int32_t N, int32_t d, int32_t V, int32_t kind,
+                                 int32_t n, float inv_c, float clamp, int32_t dtype,
+                                 void* stream) {
+  if (int32_t rc = check_head(h, E, targets, N, d, V, kind, n, dtype)) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  if (dE == nullptr) return fail("head_bwd: null dE");
+  if (N == 0) return fill_f32(dE, (int64_t)V * d, 0.0f, s);
+  if (stat == nullptr || scale == nullptr || dh == nullptr || workspace == nullptr)
+    return fail("head_bwd: null pointer");
+  const int log2n = kind == ALGX_HEAD_ALG_CE ? ilog2(n) : 0;
+  const int64_t ldz = vpad_of(V);
+  const int csize = chunk_tokens(N, V);
+  bf16* dz = (bf16*)workspace;
+  const bf16* hb = (const bf16*)h;
+  const bf16* eb = (const bf16*)E;
+  for (int tok0 = 0; tok0 < N; tok0 += csize) {
+    const int ntok = min(csize, N - tok0);
+    dim3 gdz((ntok + BN - 1) / BN, (V + BM - 1) / BM);
+    if (kind == ALGX_HEAD_CE)
+      head_dz_kernel<ALGX_HEAD_CE><<<gdz, kThreads, 0, s>>>(hb, eb, targets, stat, scale, dz, ldz,
+                                                           tok0, ntok, d, V, log2n, inv_c, clamp);
+    else
+      head_dz_kernel<ALGX_HEAD_ALG_CE><<<gdz, kThreads, 0, s>>>(
+          hb, eb, targets, stat, scale, dz, ldz, tok0, ntok, d, V, log2n, inv_c, clamp);
+    if (int32_t rc = check_launch("head_dz")) return rc;
+    // dh[t][c] = sum_v dz[t][v] E[v][c]: A = dz (k-contiguous), B(n=c,k=v) = E stored [v][c].
+    {
+      const Operand A{dz, ldz, ntok, V};
+      const Operand B{eb, d, d, V};
+      dim3 gg((d + BN - 1) / BN, (ntok + BM - 1) / BM);
+      gemm_kernel<true, false, bf16, false><<<gg, kThreads, 0, s>>>(
+          A, B, (bf16*)dh + (int64_t)tok0 * d, d, ntok, d);
+      if (int32_t rc = check_launch("head_dh")) return rc;
+    }
+    // dE[v][c] (+)= sum_t dz[t][v] h[t][c]: A(m=v,k=t) = dz stored [t][v], B(n=c,k=t) = h [t][c].
+    {
+      const Operand A{dz, ldz, V, ntok};
+      const Operand B{hb + (int64_t)tok0 * d, d, d, ntok};
+      dim3 gg((d + BN - 1) / BN, (V + BM - 1) / BM);
+      if (tok0 == 0)
+        gemm_kernel<false, false, float, false><<<gg, kThreads, 0, s>>>(A, B, dE, d, V, d);
+      else
+        gemm_kernel<false, false, float, true><<<gg, kThreads, 0, s>>>(A, B, dE, d, V, d);
+      if (int32_t rc = check_launch("head_dE")) return rc;
+    }
+  }
+  return 0;
+}

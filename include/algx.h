@@ -1,0 +1,128 @@
+/*
+ * algx -- MI355X (gfx950) kernels for the algebraic-extra hot path, C ABI.
+ *
+ * Every entry point takes caller-owned device pointers, plain sizes and a
+ * hipStream_t (passed as void*), enqueues HIP kernels on that stream and
+ * returns 0, or a nonzero status with a message from algx_last_error().
+ * No entry point allocates device memory or synchronises with the host:
+ * scratch memory is a caller-provided workspace whose size the matching
+ * *_workspace_bytes() query reports. Calls on different streams/devices are
+ * independent; the library holds no state besides the thread-local error text.
+ *
+ * Layouts are row-major as the reference passes them: attention tensors are
+ * (B, H, T, D); the head takes hidden states (N, d) and the tied embedding
+ * (V, d); QK-norm takes rows of D=64 values.
+ */
+#ifndef ALGX_H
+#define ALGX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ALGX_BF16 = 0, ALGX_F32 = 1 };
+enum { ALGX_SOFTMAX = 0, ALGX_ASINH = 1 };
+enum { ALGX_HEAD_CE = 0, ALGX_HEAD_ALG_CE = 1 };
+
+/* Numeric variant of the attention kernels; mirrors the numeric fields of the
+ * reference's Variant (src/algebraic/kernels/flash.py:59-73). Schedule flags
+ * of the reference (resident_bwd, diagonal_*, head_resident, compact_stat)
+ * select TPU schedules only and have no counterpart here. */
+typedef struct {
+  int32_t kind;            /* ALGX_SOFTMAX or ALGX_ASINH                       */
+  int32_t n;               /* asinh power, a power of two >= 2                 */
+  int32_t shift;           /* running-maximum accumulation                     */
+  int32_t fast_rho;        /* x + sqrt(1+x^2) without the negative-x reciprocal */
+  int32_t inv_stat;        /* unshifted statistic 1/Z instead of Z^(-1/n)      */
+  int32_t bounded_scores;  /* guard passed: no clamp of scores                 */
+  int32_t precise_output;  /* also write the float32 output (o_precise)        */
+  float clamp;             /* score clamp when !shift && !bounded_scores       */
+} algx_attn_variant;
+
+/* Text of the last error on this thread ("" when none). */
+const char* algx_last_error(void);
+/* Library ABI version (increments on incompatible changes). */
+int32_t algx_version(void);
+/* Diagnostic without a reference counterpart: one 32x32x16 bf16 MFMA with the
+ * lane layout every MFMA kernel of the library assumes. a: 32x16 bf16 (row
+ * major), bt: B^T as 32x16 bf16 (row major), d: 32x32 float32 = a @ b. */
+int32_t algx_selftest_mfma32(const void* a, const void* bt, float* d, void* stream);
+
+/* ---------------------------------------------------------------- QK norm
+ * Replaces qk_rms_norm (src/algebraic/kernels/qk_norm.py:62-76) with its
+ * custom VJP (:29-59) and the rms_norm math (src/algebraic/algebraic.py:76-83):
+ *   y = cast(x * rsqrt(mean(x^2) + eps) * gain)
+ * x, y, dy, dx: rows x D (D = 64), dtype ALGX_BF16 or ALGX_F32; gain, dgain: D
+ * float32. */
+int32_t algx_qknorm_fwd(const void* x, const float* gain, void* y, int64_t rows, int32_t D,
+                        int32_t dtype, float eps, void* stream);
+int64_t algx_qknorm_bwd_workspace_bytes(int64_t rows, int32_t D, int32_t dtype);
+int32_t algx_qknorm_bwd(const void* x, const float* gain, const void* dy, void* dx, float* dgain,
+                        void* workspace, int64_t rows, int32_t D, int32_t dtype, float eps,
+                        void* stream);
+
+/* -------------------------------------------------------------- attention
+ * Replaces flash_attention's device work (src/algebraic/kernels/flash.py:763-857):
+ * the range-guard reductions (:834-849), the forward kernels (_forward :292-326,
+ * head_resident.forward head_resident.py:138-155) and the custom VJP
+ * (_flash_bwd :718-726, _backward :630-687, head_resident.backward :158-176).
+ *
+ * q, k, v, o, dout, dq, dk, dv: (B, H, T, D) in `dtype`. The query is passed
+ * UNSCALED; kernels form q_s = cast(q * q_scale) on load exactly as
+ * flash.py:833 does. sink: (H,) float32 in kernel units (sink_logit / c), or
+ * NULL. stat: (B, H, T) float32.
+ *
+ * Guarded dispatch (flash.py:834-856): algx_attn_guard reduces max|q_s|^2,
+ * max|k|^2, max|v| and |sink| into `guard` (algx_attn_guard_words() int32
+ * words) and sets guard[0] = 1 when in range. Passing that buffer to the
+ * forward/backward selects `low` when guard[0] == 1 and `high` otherwise, on
+ * the device, without a host round trip. Passing guard = NULL runs `low`. */
+int32_t algx_attn_guard_words(void);
+int32_t algx_attn_guard(const void* q, const void* k, const void* v, const float* sink,
+                        int32_t* guard, int32_t B, int32_t H, int32_t T, int32_t D,
+                        int32_t dtype, float q_scale, float bound, float vmax, void* stream);
+
+/* o_precise: float32 (B,H,T,D), written only by a variant with
+ * precise_output (may be NULL when no such variant can run). */
+int32_t algx_attn_fwd(const void* q, const void* k, const void* v, const float* sink,
+                      void* o, float* o_precise, float* stat, int32_t B, int32_t H, int32_t T,
+                      int32_t D, int32_t dtype, float q_scale, const algx_attn_variant* low,
+                      const algx_attn_variant* high, const int32_t* guard, void* stream);
+
+int64_t algx_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t T, int32_t D);
+/* dq is w.r.t. the unscaled q: dq = cast(cast(dq_s) * q_scale) as autodiff of
+ * flash.py:833 gives; dsink (H,) float32 is w.r.t. the kernel-unit sink
+ * (flash.py:721-723) and may be NULL when sink is NULL. */
+int32_t algx_attn_bwd(const void* q, const void* k, const void* v, const float* sink,
+                      const void* o, const float* o_precise, const float* stat, const void* dout,
+                      void* dq, void* dk, void* dv, float* dsink, void* workspace, int32_t B,
+                      int32_t H, int32_t T, int32_t D, int32_t dtype, float q_scale,
+                      const algx_attn_variant* low, const algx_attn_variant* high,
+                      const int32_t* guard, void* stream);
+
+/* ------------------------------------------------------------ fused head
+ * Replaces fused_head (src/algebraic/kernels/fused_head.py:260-275): forward
+ * statistics (_forward :174-191: stat = logsumexp or Z^(-1/n), zt = target
+ * logit) and the backward (_backward :194-216), without materialising the
+ * (N, V) logits. h: (N, d) and E: (V, d) in `dtype` (the reference casts E to
+ * h's dtype, :168); targets int32 (N,); stat, zt float32 (N,).
+ * scale: device float32 scalar g * (1 or n/c) / N (fused_head.py:251).
+ * dh: (N, d) in dtype; dE: (V, d) float32. The MFMA kernels take bf16 (dtype
+ * ALGX_BF16) hidden states with d % 8 == 0; V is arbitrary (ragged tail masked). */
+int64_t algx_head_fwd_workspace_bytes(int32_t N, int32_t d, int32_t V, int32_t dtype);
+int32_t algx_head_fwd(const void* h, const void* E, const int32_t* targets, float* stat,
+                      float* zt, void* workspace, int32_t N, int32_t d, int32_t V, int32_t kind,
+                      int32_t n, float inv_c, float clamp, int32_t dtype, void* stream);
+int64_t algx_head_bwd_workspace_bytes(int32_t N, int32_t d, int32_t V, int32_t dtype);
+int32_t algx_head_bwd(const void* h, const void* E, const int32_t* targets, const float* stat,
+                      const float* scale, void* dh, float* dE, void* workspace, int32_t N,
+                      int32_t d, int32_t V, int32_t kind, int32_t n, float inv_c, float clamp,
+                      int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ALGX_H */

@@ -1,0 +1,109 @@
+"""C-ABI boundary and host-side checks that need no GPU.
+
+* libalgx.so loads and exports every entry point include/algx.h declares;
+* host-only queries (workspace sizes, guard words) answer;
+* the Python operators raise the reference's ValueErrors before any device
+  work (flash.py:796-817, fused_head.py:269-272, qk_norm.py:68-75).
+"""
+
+import os
+import re
+
+import pytest
+import torch
+
+from algebraic_amd import _lib
+from algebraic_amd.kernels import flash_attention, fused_head, make_variant, qk_rms_norm
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "algx.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(algx_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declarations_match_binding():
+    names = _declared()
+    assert "algx_attn_fwd" in names and "algx_head_bwd" in names and "algx_qknorm_fwd" in names
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+
+
+def test_library_loads_and_exports_every_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.algx_version() == 1
+    assert lib.algx_last_error() == b""
+
+
+def test_host_queries():
+    assert _lib.query("algx_attn_guard_words") >= 8
+    assert _lib.query("algx_attn_bwd_workspace_bytes", 8, 12, 2048, 64) >= 8 * 12 * 2048 * 64 * 4
+    assert _lib.query("algx_qknorm_bwd_workspace_bytes", 1 << 18, 64, 0) > 0
+    assert _lib.query("algx_head_fwd_workspace_bytes", 16384, 768, 50304, 0) > 0
+    assert _lib.query("algx_head_bwd_workspace_bytes", 16384, 768, 50304, 0) > 0
+
+
+def test_entry_points_reject_bad_arguments_without_a_gpu():
+    """Validation happens before any launch: a bad dtype or size returns an error."""
+    lib = _lib.load()
+    rc = lib.algx_qknorm_fwd(None, None, None, 16, 32, 0, 1e-5, None)
+    assert rc != 0 and b"D must be 64" in lib.algx_last_error()
+    v = _lib.AttnVariant(kind=1, n=12)
+    rc = lib.algx_attn_fwd(None, None, None, None, None, None, None, 1, 1, 128, 64, 0, 1.0,
+                           v, None, None, None)
+    assert rc != 0 and b"power of two" in lib.algx_last_error()
+    rc = lib.algx_head_fwd(None, None, None, None, None, None, 4, 12, 100, 0, 16, 1.0, 0.0, 0, None)
+    assert rc != 0 and b"multiple of 8" in lib.algx_last_error()
+
+
+def _t(shape, dtype=torch.bfloat16):
+    return torch.zeros(shape, dtype=dtype)
+
+
+def test_flash_validation_mirrors_reference():
+    x = _t((1, 1, 512, 64))
+    with pytest.raises(ValueError, match="divisible by blocks"):
+        flash_attention(_t((1, 1, 384, 64)), _t((1, 1, 384, 64)), _t((1, 1, 384, 64)),
+                        kind="asinh", block=256)
+    with pytest.raises(ValueError, match="whole-head residency"):
+        flash_attention(x, x, x, kind="asinh", c=8., head_resident=True)   # test_flash_kernel_tpu.py:331-335
+    with pytest.raises(ValueError, match="resident backward needs"):
+        flash_attention(_t((1, 1, 256, 64)), _t((1, 1, 256, 64)), _t((1, 1, 256, 64)),
+                        kind="asinh", resident_bwd=True)
+    with pytest.raises(ValueError, match="diagonal backward requires"):
+        flash_attention(x, x, x, kind="asinh", resident_bwd=False, diagonal_bwd=True)
+    with pytest.raises(ValueError, match="power of two"):
+        flash_attention(x, x, x, kind="asinh", n=12)
+    with pytest.raises(ValueError, match="unknown attention kernel"):
+        flash_attention(x, x, x, kind="relu")
+    with pytest.raises(NotImplementedError, match="poly_rho"):
+        flash_attention(x, x, x, kind="asinh", n=16, shift=False, poly_rho=True)
+
+
+def test_make_variant_matches_reference_defaults():
+    v = make_variant("asinh", 16, 8.0, 2048)
+    assert abs(v.clamp - 63.75) < 5e-3 and not v.shift and v.inv_stat and v.fast_rho
+    assert make_variant("asinh", 32, 8.0, 2048).shift
+    assert make_variant("softmax").kind == "softmax"
+
+
+def test_head_and_norm_validation_mirror_reference():
+    h, e, t = _t((256, 64)), torch.zeros((512, 64)), torch.zeros(256, dtype=torch.int64)
+    with pytest.raises(ValueError):
+        fused_head(h, e, t, kind="mse")
+    with pytest.raises(ValueError, match="power of two"):
+        fused_head(h, e, t, kind="alg_ce", n=12)
+    with pytest.raises(ValueError, match="divisible by block"):
+        fused_head(_t((200, 64)), e, t[:200], block_n=128)
+    g = torch.ones(64)
+    with pytest.raises(ValueError, match="D=64"):
+        qk_rms_norm(_t((4, 32)), torch.ones(32))
+    with pytest.raises(ValueError, match="float32/BF16"):
+        qk_rms_norm(_t((1024, 64), torch.float16), g)
+    with pytest.raises(ValueError, match="divisible by a block"):
+        qk_rms_norm(_t((1000, 64)), g, block=1024)
+    with pytest.raises(ValueError, match="positive"):
+        qk_rms_norm(_t((1024, 64)), g, eps=0.0)

@@ -1,0 +1,234 @@
+"""GPU parity of flash_attention (HIP) against the CPU oracle.
+
+Mirrors the reference's TPU suite (tests/test_flash_kernel_tpu.py): the
+variant cases of test_flash_matches_dense, the model statistics modes, the
+guarded tails, the clip VJP, and the whole-head model shape; plus
+size-independent properties at the benchmark shape (cfg2/cfg4: B=8, T=2048).
+Tolerances: tests/_tol.py (float32 rtol 1e-4; bf16 2e-2 max-abs, 1e-2 rel-L2).
+"""
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from _tol import assert_bf16, assert_dtype_close, assert_f32, rel_l2, to_np
+from algebraic_amd import _lib
+from algebraic_amd.kernels import flash_attention
+from oracle import attention as OA
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TORCH_DT = {"bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def _rand(shape, seed, scale=1.0, dtype="bf16", n=4):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        x = torch.from_numpy((rng.standard_normal(shape) * scale).astype(np.float32))
+        out.append(x.to(TORCH_DT[dtype]))
+    return out
+
+
+def _run(q, k, v, g, sink, **kw):
+    """Forward + VJP on the GPU; returns numpy (o, dq, dk, dv, dsink)."""
+    tq, tk, tv = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
+    ts = None if sink is None else torch.as_tensor(sink, dtype=torch.float32, device=DEV).requires_grad_(True)
+    o = flash_attention(tq, tk, tv, ts, **kw)
+    (o.float() * g.to(DEV).float()).sum().backward()
+    torch.cuda.synchronize()
+    return (to_np(o), to_np(tq.grad), to_np(tk.grad), to_np(tv.grad),
+            None if ts is None else to_np(ts.grad))
+
+
+def _oracle(q, k, v, g, sink, dtype, **kw):
+    res = OA.flash_attention(to_np(q), to_np(k), to_np(v), None if sink is None else to_np(sink),
+                             dtype=dtype, do=to_np(g), **kw)
+    return (res.o,) + tuple(res.grads), res
+
+
+def _check_all(got, want, dtype, names=("o", "dq", "dk", "dv", "dsink")):
+    for a, b, nm in zip(got, want, names):
+        if a is None and b is None:
+            continue
+        if nm == "dsink":
+            # float32 reduction over B*T rows in both implementations.
+            assert rel_l2(a, b) <= (1e-4 if dtype == "f32" else 1e-2), (nm, a, b)
+            continue
+        assert_dtype_close(a, b, dtype, what=nm)
+
+
+def test_mfma_lane_layout_selftest():
+    """One v_mfma_f32_32x32x16_bf16 with the layout all MFMA kernels assume."""
+    rng = np.random.default_rng(0)
+    a = torch.from_numpy(rng.standard_normal((32, 16)).astype(np.float32)).to(torch.bfloat16)
+    bt = torch.from_numpy(rng.standard_normal((32, 16)).astype(np.float32)).to(torch.bfloat16)
+    d = torch.empty((32, 32), dtype=torch.float32, device=DEV)
+    ad, btd = a.to(DEV), bt.to(DEV)
+    _lib.call("algx_selftest_mfma32", _lib.ptr(ad), _lib.ptr(btd), _lib.ptr(d), _lib.stream())
+    torch.cuda.synchronize()
+    want = a.double().numpy() @ bt.double().numpy().T
+    np.testing.assert_allclose(d.cpu().numpy(), want, rtol=1e-5, atol=1e-5)
+
+
+# test_flash_kernel_tpu.py:33-35 plus the model preset and the softmax arm
+CASES = [("asinh", 16, 16.0, True, True, False), ("asinh", 16, 16.0, True, True, True),
+         ("asinh", 16, 16.0, True, False, True), ("asinh", 16, 16.0, False, False, True),
+         ("asinh", 8, 1.0, True, True, False), ("asinh", 32, 8.0, False, True, True),
+         ("softmax", 16, 16.0, True, None, None), ("softmax", 16, 16.0, False, None, None)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("kind,n,c,with_sink,shift,fast", CASES)
+def test_flash_matches_oracle(kind, n, c, with_sink, shift, fast, dtype):
+    """Every explicit variant, both dtypes, B,H,T,D = 2,3,256,64, inputs x1.5."""
+    shape = (2, 3, 256, 64)
+    q, k, v, g = _rand(shape, 0, dtype=dtype)
+    q, k = ((x.float() * 1.5).to(TORCH_DT[dtype]) for x in (q, k))
+    sink = (torch.from_numpy(np.random.default_rng(4).standard_normal(3).astype(np.float32)) * 0.5
+            ).reshape(1, 3, 1, 1) if with_sink else None
+    kw = dict(kind=kind, n=n, c=c, shift=shift, fast_rho=fast)
+    got = _run(q, k, v, g, sink, block=128, **kw)
+    want, res = _oracle(q, k, v, g, sink, dtype, **kw)
+    _check_all(got, want, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("mode", ["root", "inverse", "guarded"])
+def test_model_attention_statistics(mode, dtype):
+    """test_flash_kernel_tpu.py:69-97: n=16, c=8 with a sink, statistic modes."""
+    shape = (1, 2, 512, 64)
+    q, k, v, g = _rand(shape, 13, dtype=dtype)
+    sink = torch.from_numpy(np.random.default_rng(14).standard_normal((1, 2, 1, 1)).astype(np.float32))
+    kw = dict(kind="asinh", n=16, c=8.0, shift=False, fast_rho=True, inv_stat=mode != "root",
+              range_guard=mode == "guarded")
+    got = _run(q, k, v, g, sink, block_q=128, block_k=256, **kw)
+    want, res = _oracle(q, k, v, g, sink, dtype, **kw)
+    if mode == "guarded":
+        assert res.in_range
+    _check_all(got, want, dtype)
+    # the reference's own check against the dense function (0.012 / rel 0.02|0.005)
+    dense = OA.dense_asinh_attention(to_np(q), to_np(k), to_np(v), n=16, c=8.0, sink_logit=to_np(sink),
+                                     p_dtype=dtype)
+    np.testing.assert_allclose(got[0], dense, atol=0.012, rtol=0.012)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("score_sign", [-1.0, 1.0])
+@pytest.mark.parametrize("with_sink", [False, True])
+@pytest.mark.parametrize("magnitude", [1000.0, 1e7])
+def test_guarded_attention_tail(score_sign, with_sink, magnitude, dtype):
+    """test_flash_kernel_tpu.py:100-119: guarded fallback for overflow and underflow."""
+    shape = (1, 1, 256, 64)
+    q = torch.full(shape, math.sqrt(magnitude), dtype=TORCH_DT[dtype])
+    k = (q.float() * score_sign).to(TORCH_DT[dtype])
+    v = _rand(shape, 29, dtype=dtype, n=1)[0]
+    g = torch.ones(shape, dtype=TORCH_DT[dtype])
+    sink = torch.zeros((1,)) if with_sink else None
+    kw = dict(kind="asinh", n=16, c=8.0, range_guard=True)
+    got = _run(q, k, v, g, sink, block=128, **kw)
+    want, res = _oracle(q, k, v, g, sink, dtype, **kw)
+    assert res.in_range is False
+    assert all(np.isfinite(x).all() for x in got[:4])
+    dense = OA.dense_asinh_attention(to_np(q), to_np(k), to_np(v), n=16, c=8.0,
+                                     sink_logit=None if sink is None else to_np(sink), p_dtype=dtype)
+    tol = 2e-3 if dtype == "f32" else 0.012
+    np.testing.assert_allclose(got[0], dense, atol=tol, rtol=tol)
+    assert_dtype_close(got[0], want[0], dtype, what="o")
+
+
+def test_explicit_clipping_vjp_is_zero_above_cap():
+    """test_flash_kernel_tpu.py:122-138: saturated scores and sink have zero VJP."""
+    shape = (1, 1, 256, 64)
+    q = torch.full(shape, math.sqrt(1000), dtype=torch.float32)
+    v, g = _rand(shape, 39, dtype="f32", n=2)
+    got = _run(q, q.clone(), v, g, torch.full((1,), 1000.0), kind="asinh", n=16, c=8.0,
+               block=128, shift=False, range_guard=False)
+    for x in (got[1], got[2], got[4]):
+        assert np.all(x == 0)
+
+
+@pytest.mark.parametrize("mode", ["sink", "no_sink", "negative", "gain_two", "positive_tail",
+                                  "negative_tail"])
+def test_whole_head_model_shape(mode):
+    """test_flash_kernel_tpu.py:253-328 at (1, 2, 2048, 64) bf16, guarded n=16, c=8."""
+    shape = (1, 2, 2048, 64)
+    q, k, v, g = _rand(shape, 563)
+    sink = torch.tensor([-0.35, 0.125]).reshape(1, 2, 1, 1)
+    if mode in ("no_sink", "negative"):
+        sink = None
+    if mode == "negative":
+        q = (1 + 0.05 * q.float()).to(torch.bfloat16)
+        k = (-1 + 0.05 * k.float()).to(torch.bfloat16)
+    if mode == "gain_two":
+        q = (2 * q.float() * torch.rsqrt((q.float() ** 2).mean(-1, keepdim=True) + 1e-5)).to(torch.bfloat16)
+        k = (2 * k.float() * torch.rsqrt((k.float() ** 2).mean(-1, keepdim=True) + 1e-5)).to(torch.bfloat16)
+    if mode.endswith("tail"):
+        q = torch.full(shape, math.sqrt(1000), dtype=torch.bfloat16)
+        k = q if mode == "positive_tail" else (-q.float()).to(torch.bfloat16)
+    kw = dict(kind="asinh", n=16, c=8.0, range_guard=True)
+    got = _run(q, k, v, g, sink, **kw)
+    want, res = _oracle(q, k, v, g, sink, "bf16", **kw)
+    assert res.in_range == (not mode.endswith("tail"))
+    names = ("o", "dq", "dk", "dv", "dsink")
+    for a, b, nm in zip(got, want, names):
+        if a is None:
+            continue
+        if nm == "dq" and mode in ("positive_tail", "negative"):
+            # Equal or nearly common scores make dQ a small difference of bf16-rounded
+            # terms (test_flash_kernel_tpu.py:205-207, :295-314): absolute check only.
+            assert np.abs(a - b).max() <= 2e-2, (mode, np.abs(a - b).max())
+            continue
+        if nm == "dsink":
+            assert rel_l2(a, b) <= 1e-2
+            continue
+        assert_bf16(a, b, what=f"{mode}:{nm}")
+
+
+def test_mfma_path_matches_generic_kernels():
+    """The MFMA kernels and the scalar kernels agree on every output (bf16, T=512)."""
+    shape = (2, 4, 512, 64)
+    q, k, v, g = _rand(shape, 77)
+    sink = torch.tensor([0.3, -0.2, 0.0, 1.0]).reshape(1, 4, 1, 1)
+    kw = dict(kind="asinh", n=16, c=8.0, range_guard=True)
+    fast = _run(q, k, v, g, sink, **kw)
+    os.environ["ALGX_FORCE_GENERIC"] = "1"
+    try:
+        slow = _run(q, k, v, g, sink, **kw)
+    finally:
+        del os.environ["ALGX_FORCE_GENERIC"]
+    for a, b, nm in zip(fast, slow, ("o", "dq", "dk", "dv", "dsink")):
+        assert rel_l2(a, b) <= 5e-3, (nm, rel_l2(a, b))
+
+
+@pytest.mark.parametrize("H", [12, 16])
+def test_benchmark_shape_properties(H):
+    """cfg2/cfg4 shape (8, H, 2048, 64) bf16, QK-normed inputs, guarded n=16, c=8:
+    the in-range path runs; outputs are finite; weights sum to one (v = 1 gives
+    o = 1); the output is causal (perturbing later keys leaves earlier rows
+    unchanged); and one head matches the oracle."""
+    B, T, D = 8, 2048, 64
+    shape = (B, H, T, D)
+    gen = torch.Generator(device=DEV).manual_seed(1)
+    q = torch.randn(shape, device=DEV, generator=gen)
+    k = torch.randn(shape, device=DEV, generator=gen)
+    q = (q * torch.rsqrt((q * q).mean(-1, keepdim=True) + 1e-5)).bfloat16()
+    k = (k * torch.rsqrt((k * k).mean(-1, keepdim=True) + 1e-5)).bfloat16()
+    v = torch.randn(shape, device=DEV, generator=gen).bfloat16()
+    kw = dict(kind="asinh", n=16, c=8.0, range_guard=True)
+    o = flash_attention(q, k, v, **kw)
+    assert torch.isfinite(o.float()).all()
+    ones = flash_attention(q, k, torch.ones_like(v), **kw).float()
+    assert (ones - 1).abs().max().item() <= 8e-3
+    k2 = k.clone()
+    k2[:, :, 1024:] = (k2[:, :, 1024:].float() * -3).bfloat16()
+    o2 = flash_attention(q, k2, v, **kw)
+    assert torch.equal(o[:, :, :1024], o2[:, :, :1024])
+    # one head against the oracle
+    qs, ks, vs = (x[3:4, 5:6].cpu() for x in (q, k, v))
+    res = OA.flash_attention(to_np(qs), to_np(ks), to_np(vs), None, dtype="bf16", **kw)
+    assert res.in_range
+    assert_bf16(o[3:4, 5:6], res.o, what="o(head)")

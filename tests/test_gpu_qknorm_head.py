@@ -1,0 +1,112 @@
+"""GPU parity of qk_rms_norm and fused_head (HIP) against the CPU oracle.
+
+Mirrors tests/test_qk_norm_tpu.py:21-43 and tests/test_fused_head_tpu.py:13-67
+of the reference, at the tolerances of tests/_tol.py.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _tol import assert_bf16, assert_f32, rel_l2, to_np
+from algebraic_amd.kernels import fused_head, qk_rms_norm
+from oracle import head as OH
+from oracle import qknorm as OQ
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("eps", [1e-5, 1e-3])
+@pytest.mark.parametrize("shape", [(2, 3, 512, 64), (8, 16, 2048, 64)])
+def test_qk_norm_output_and_vjp(dtype, eps, shape):
+    """x = 3 N(0,1) with row 0 zeroed, gain in .25 + 4 U(0,1) (qk_norm TPU test)."""
+    rng = np.random.default_rng(181)
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    x = torch.from_numpy((3 * rng.standard_normal(shape)).astype(np.float32)).to(tdt)
+    x[0, 0, 0] = 0
+    gain = torch.from_numpy((0.25 + 4 * rng.random(64)).astype(np.float32))
+    dy = torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(tdt)
+    tx = x.to(DEV).requires_grad_(True)
+    tg = gain.to(DEV).requires_grad_(True)
+    y = qk_rms_norm(tx, tg, eps, block=256)
+    (y.float() * dy.to(DEV).float()).sum().backward()
+    torch.cuda.synchronize()
+    big = shape[0] > 2
+    sl = (slice(0, 1), slice(0, 2)) if big else (slice(None),)
+    want_y = OQ.forward(to_np(x[sl]), to_np(gain), eps, dtype)
+    want_dx, _ = OQ.backward(to_np(x[sl]), to_np(gain), to_np(dy[sl]), eps, dtype)
+    check = assert_f32 if dtype == "f32" else assert_bf16
+    check(y[sl], want_y, what="y")
+    check(tx.grad[sl], want_dx, what="dx")
+    if not big:
+        _, want_dg = OQ.backward(to_np(x), to_np(gain), to_np(dy), eps, dtype)
+        assert rel_l2(tg.grad, want_dg) <= (1e-5 if dtype == "f32" else 1e-3)
+    else:
+        # dgain over 16.8M rows: compare with a float64 torch reduction on the GPU.
+        xf = x.to(DEV).double()
+        tau = torch.rsqrt((xf * xf).mean(-1, keepdim=True) + eps)
+        dg = (dy.to(DEV).double() * xf * tau).reshape(-1, 64).sum(0)
+        assert rel_l2(tg.grad, dg) <= 1e-4
+
+
+def _head_inputs(N, d, V, seed, escale):
+    rng = np.random.default_rng(seed)
+    h = torch.from_numpy(rng.standard_normal((N, d)).astype(np.float32)).bfloat16()
+    e = torch.from_numpy((rng.standard_normal((V, d)) * escale).astype(np.float32))
+    t = torch.from_numpy(rng.integers(0, V, N).astype(np.int64))
+    return h, e, t
+
+
+def _head_run(h, e, t, **kw):
+    th, te = h.to(DEV).requires_grad_(True), e.to(DEV).requires_grad_(True)
+    obj, tel = fused_head(th, te, t.to(DEV), **kw)
+    obj.backward()
+    torch.cuda.synchronize()
+    return float(obj), to_np(tel), to_np(th.grad), to_np(te.grad)
+
+
+@pytest.mark.parametrize("kind,n,c", [("alg_ce", 16, 16.0), ("alg_ce", 8, 2.0), ("ce", 16, 16.0)])
+@pytest.mark.parametrize("V", [4096, 32768, 1000])
+def test_fused_head_matches_oracle(kind, n, c, V):
+    """N=1024, d=256, E ~ 0.15 N(0,1) (test_fused_head_tpu.py:13-40), plus a ragged V."""
+    h, e, t = _head_inputs(1024, 256, V, 0, 0.15)
+    got = _head_run(h, e, t, kind=kind, n=n, c=c, block_n=256, block_v=1024)
+    (obj, tel), (dh, de) = OH.fused_head(to_np(h), to_np(e), to_np(t), kind=kind, n=n, c=c,
+                                         dtype="bf16", g_obj=1.0)
+    assert abs(got[0] - obj) <= 2e-4 + 2e-3 * abs(obj)
+    np.testing.assert_allclose(got[1], tel, rtol=2e-2, atol=2e-4)
+    assert_bf16(got[2], dh, what="dh")
+    assert rel_l2(got[3], de) <= 1e-2
+    # reference's own check: max-normalised agreement and cosine
+    for a, b in ((got[2], dh), (got[3], de)):
+        scale = np.abs(b).max() + 1e-12
+        np.testing.assert_allclose(a / scale, b / scale, atol=2e-2)
+        cos = (a * b).sum() / np.sqrt((a * a).sum() * (b * b).sum())
+        assert cos > 0.999
+
+
+@pytest.mark.parametrize("width", [768, 1024])
+def test_production_head_tiles_at_model_widths(width):
+    """test_fused_head_tpu.py:43-67: 256 tokens, V=32768, E ~ 0.02 N(0,1), n=8, c=2."""
+    h, e, t = _head_inputs(256, width, 32768, 42, 0.02)
+    got = _head_run(h, e, t, kind="alg_ce", n=8, c=2.0)
+    (obj, tel), (dh, de) = OH.fused_head(to_np(h), to_np(e), to_np(t), kind="alg_ce", n=8, c=2.0,
+                                         dtype="bf16", g_obj=1.0)
+    assert abs(got[0] - obj) <= 2e-4 + 2e-3 * abs(obj)
+    assert rel_l2(got[2], dh) < 0.01 and rel_l2(got[3], de) < 0.01
+
+
+def test_fused_head_alg_gradient_is_log_loss_gradient():
+    """The alg_ce VJP equals the exact NLL gradient of log_softmax(n asinh(z/c))."""
+    h, e, t = _head_inputs(256, 128, 4096, 9, 0.3)
+    got = _head_run(h, e, t, kind="alg_ce", n=8, c=2.0)
+    th = torch.tensor(to_np(h), requires_grad=True)
+    te = torch.tensor(to_np(e.bfloat16()), requires_grad=True)
+    z = th @ te.T
+    logp = torch.log_softmax(8 * torch.asinh(z / 2.0), -1)[torch.arange(256), t]
+    (-logp.mean()).backward()
+    assert rel_l2(got[2], th.grad.numpy()) < 1e-2
+    assert rel_l2(got[3], te.grad.numpy()) < 1e-2
+    np.testing.assert_allclose(got[1], np.exp(logp.detach().numpy()), rtol=2e-2, atol=2e-6)
