@@ -21,6 +21,12 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "algebraic_amd", "libalgx.so")
 ARCH = "gfx950"
+# Extra flags per translation unit: the MFMA kernels keep their accumulators in
+# architectural VGPRs so the VALU reads them without accvgpr copies.
+EXTRA = {
+    "attn_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "head.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def hipcc():
@@ -43,13 +49,14 @@ def flags():
 
 def _compile(src, asm):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [hipcc()] + flags() + ["-c", src, "-o", obj]
+    extra = EXTRA.get(os.path.basename(src), [])
+    cmd = [hipcc()] + flags() + extra + ["-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {src}\n{res.stderr}")
     if asm:
         s = os.path.join(BUILD, os.path.basename(src) + ".s")
-        subprocess.run([hipcc()] + flags() + ["--cuda-device-only", "-S", src, "-o", s],
+        subprocess.run([hipcc()] + flags() + extra + ["--cuda-device-only", "-S", src, "-o", s],
                        capture_output=True, text=True, check=True)
     return obj
 

@@ -80,7 +80,17 @@ __device__ __forceinline__ bf16x8 scale_bf16x8(bf16x8 x, float s) {
   return y;
 }
 
-template <int MODE, bool FAST, bool BOUNDED>
+// x^(2^log2n) with a compile-time exponent when L2N > 0.
+template <int L2N> __device__ __forceinline__ float powN(float x, int log2n) {
+  if (L2N > 0) {
+#pragma unroll
+    for (int i = 0; i < L2N; ++i) x = x * x;
+    return x;
+  }
+  return pow2n(x, log2n);
+}
+
+template <int MODE, bool FAST, bool BOUNDED, int L2N>
 __global__ __launch_bounds__(256) void fwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
@@ -187,7 +197,7 @@ __global__ __launch_bounds__(256) void fwd_mfma_kernel(
             const float s = sacc[mt][r];
             const float x = BOUNDED ? s : __builtin_fminf(s, var.clamp);
             float rr;
-            float p = pow2n(FAST ? rho_fast(x, rr) : rho_exact(x, rr), log2n);
+            float p = powN<L2N>(FAST ? rho_fast(x, rr) : rho_exact(x, rr), log2n);
             if (diag) {
               const int key = k0 + 32 * mt + 8 * (r >> 2) + 4 * g + (r & 3);
               if (key > qrow) p = 0.0f;
@@ -231,13 +241,13 @@ __global__ __launch_bounds__(256) void fwd_mfma_kernel(
         } else {
           float rr;
           const float shf = rho_exact(-m_new, rr);
-          alpha = pow2n(rho_exact(m_prev, rr) * shf, log2n);
+          alpha = powN<L2N>(rho_exact(m_prev, rr) * shf, log2n);
 #pragma unroll
           for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const float s = sacc[mt][r];
-              float p = pow2n((FAST ? rho_fast(s, rr) : rho_exact(s, rr)) * shf, log2n);
+              float p = powN<L2N>((FAST ? rho_fast(s, rr) : rho_exact(s, rr)) * shf, log2n);
               if (s == -__builtin_inff()) p = 0.0f;
               sacc[mt][r] = p;
               lsum += p;
@@ -289,7 +299,7 @@ __global__ __launch_bounds__(256) void fwd_mfma_kernel(
 }
 
 // p and ds of one score (flash.py:339-361); ds already multiplied by r.
-template <int MODE, bool FAST, bool BOUNDED>
+template <int MODE, bool FAST, bool BOUNDED, int L2N>
 __device__ __forceinline__ void tile_grad(float s, float dp, float st, float dd, float clamp,
                                           int log2n, bool inv_stat, float& p, float& ds) {
   if (MODE == MODE_SOFTMAX) {
@@ -300,13 +310,13 @@ __device__ __forceinline__ void tile_grad(float s, float dp, float st, float dd,
   const float x = (MODE == MODE_NOSHIFT && !BOUNDED) ? __builtin_fminf(s, clamp) : s;
   float r;
   const float rh = FAST ? rho_fast(x, r) : rho_exact(x, r);
-  p = (MODE == MODE_NOSHIFT && inv_stat) ? pow2n(rh, log2n) * st : pow2n(rh * st, log2n);
+  p = (MODE == MODE_NOSHIFT && inv_stat) ? powN<L2N>(rh, log2n) * st : powN<L2N>(rh * st, log2n);
   ds = p * (dp - dd) * r;
   if (MODE == MODE_NOSHIFT && !BOUNDED && !(s < clamp)) ds = 0.0f;
 }
 
-template <int MODE, bool FAST, bool BOUNDED>
-__global__ __launch_bounds__(256) void bwd_mfma_kernel(
+template <int MODE, bool FAST, bool BOUNDED, int L2N>
+__global__ __launch_bounds__(256, 2) void bwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ stat, const float* __restrict__ di, const bf16* __restrict__ dout,
     float* __restrict__ dq_acc, bf16* __restrict__ dk, bf16* __restrict__ dv, int T_,
@@ -441,7 +451,7 @@ __global__ __launch_bounds__(256) void bwd_mfma_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float p, ds;
-            tile_grad<MODE, FAST, BOUNDED>(sacc[mq][4 * j + i], pacc[mq][4 * j + i], st4[i],
+            tile_grad<MODE, FAST, BOUNDED, L2N>(sacc[mq][4 * j + i], pacc[mq][4 * j + i], st4[i],
                                            di4[i], clamp, log2n, inv_stat, p, ds);
             if (diag && q0 + qo + i < kcol) {
               p = 0.0f;
@@ -534,26 +544,48 @@ typedef void (*BwdFn)(const bf16*, const bf16*, const bf16*, const float*, const
                       const bf16*, float*, bf16*, bf16*, int, float, KVariant, const int32_t*,
                       int);
 
+template <int MODE, bool FAST, bool BOUNDED>
+FwdFn fwd_by_power(int log2n) {
+  switch (log2n) {
+    case 3: return fwd_mfma_kernel<MODE, FAST, BOUNDED, 3>;
+    case 4: return fwd_mfma_kernel<MODE, FAST, BOUNDED, 4>;
+    case 5: return fwd_mfma_kernel<MODE, FAST, BOUNDED, 5>;
+    default: return fwd_mfma_kernel<MODE, FAST, BOUNDED, 0>;
+  }
+}
+
+template <int MODE, bool FAST, bool BOUNDED>
+BwdFn bwd_by_power(int log2n) {
+  switch (log2n) {
+    case 3: return bwd_mfma_kernel<MODE, FAST, BOUNDED, 3>;
+    case 4: return bwd_mfma_kernel<MODE, FAST, BOUNDED, 4>;
+    case 5: return bwd_mfma_kernel<MODE, FAST, BOUNDED, 5>;
+    default: return bwd_mfma_kernel<MODE, FAST, BOUNDED, 0>;
+  }
+}
+
 FwdFn pick_fwd(const KVariant& v) {
-  if (v.kind == ALGX_SOFTMAX) return fwd_mfma_kernel<MODE_SOFTMAX, false, false>;
+  if (v.kind == ALGX_SOFTMAX) return fwd_mfma_kernel<MODE_SOFTMAX, false, false, 1>;
   if (v.shift)
-    return v.fast ? fwd_mfma_kernel<MODE_SHIFT, true, false> : fwd_mfma_kernel<MODE_SHIFT, false, false>;
+    return v.fast ? fwd_by_power<MODE_SHIFT, true, false>(v.log2n)
+                  : fwd_by_power<MODE_SHIFT, false, false>(v.log2n);
   if (v.bounded)
-    return v.fast ? fwd_mfma_kernel<MODE_NOSHIFT, true, true>
-                  : fwd_mfma_kernel<MODE_NOSHIFT, false, true>;
-  return v.fast ? fwd_mfma_kernel<MODE_NOSHIFT, true, false>
-                : fwd_mfma_kernel<MODE_NOSHIFT, false, false>;
+    return v.fast ? fwd_by_power<MODE_NOSHIFT, true, true>(v.log2n)
+                  : fwd_by_power<MODE_NOSHIFT, false, true>(v.log2n);
+  return v.fast ? fwd_by_power<MODE_NOSHIFT, true, false>(v.log2n)
+                : fwd_by_power<MODE_NOSHIFT, false, false>(v.log2n);
 }
 
 BwdFn pick_bwd(const KVariant& v) {
-  if (v.kind == ALGX_SOFTMAX) return bwd_mfma_kernel<MODE_SOFTMAX, false, false>;
+  if (v.kind == ALGX_SOFTMAX) return bwd_mfma_kernel<MODE_SOFTMAX, false, false, 1>;
   if (v.shift)
-    return v.fast ? bwd_mfma_kernel<MODE_SHIFT, true, false> : bwd_mfma_kernel<MODE_SHIFT, false, false>;
+    return v.fast ? bwd_by_power<MODE_SHIFT, true, false>(v.log2n)
+                  : bwd_by_power<MODE_SHIFT, false, false>(v.log2n);
   if (v.bounded)
-    return v.fast ? bwd_mfma_kernel<MODE_NOSHIFT, true, true>
-                  : bwd_mfma_kernel<MODE_NOSHIFT, false, true>;
-  return v.fast ? bwd_mfma_kernel<MODE_NOSHIFT, true, false>
-                : bwd_mfma_kernel<MODE_NOSHIFT, false, false>;
+    return v.fast ? bwd_by_power<MODE_NOSHIFT, true, true>(v.log2n)
+                  : bwd_by_power<MODE_NOSHIFT, false, true>(v.log2n);
+  return v.fast ? bwd_by_power<MODE_NOSHIFT, true, false>(v.log2n)
+                : bwd_by_power<MODE_NOSHIFT, false, false>(v.log2n);
 }
 
 }  // namespace
