@@ -13,6 +13,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libalgx.so"
 BF16, F32 = 0, 1
 SOFTMAX, ASINH = 0, 1
 HEAD_CE, HEAD_ALG_CE = 0, 1
+PROBE = {"none": 0, "attn_fwd": 1, "attn_bwd": 2, "head_fwd": 3, "head_dz": 4, "head_dh": 5,
+         "head_de": 6, "qknorm_fwd": 7, "qknorm_bwd": 8}
 
 _i32, _i64, _f32, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -31,13 +33,14 @@ SIGNATURES = {
     "algx_last_error": (ctypes.c_char_p, []),
     "algx_version": (_i32, []),
     "algx_selftest_mfma32": (_i32, [_p, _p, _p, _p]),
+    "algx_set_probe": (_i32, [_i32, _p, _p]),
     "algx_qknorm_fwd": (_i32, [_p, _p, _p, _i64, _i32, _i32, _f32, _p]),
     "algx_qknorm_bwd_workspace_bytes": (_i64, [_i64, _i32, _i32]),
     "algx_qknorm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _f32, _p]),
     "algx_attn_guard_words": (_i32, []),
-    "algx_attn_guard": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _f32,
-                               _f32, _p]),
-    "algx_attn_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32,
+    "algx_attn_prepare": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32,
+                                 _f32, _f32, _p]),
+    "algx_attn_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32,
                              _VP, _VP, _p, _p]),
     "algx_attn_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "algx_attn_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,

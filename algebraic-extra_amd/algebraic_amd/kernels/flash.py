@@ -119,36 +119,38 @@ class _FlashFn(torch.autograd.Function):
         if plan.high is not None:
             words = _lib.query("algx_attn_guard_words")
             guard = torch.empty(words, dtype=torch.int32, device=dev)
-            _lib.call("algx_attn_guard", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v),
-                      _lib.ptr(sink), _lib.ptr(guard), B, H, T, D, dt, plan.q_scale,
-                      plan.bound, plan.vmax, st)
+        # q_s = cast(q * scale) (flash.py:833), plus the guard word when guarded.
+        q_s = torch.empty_like(q)
+        _lib.call("algx_attn_prepare", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
+                  _lib.ptr(q_s), _lib.ptr(guard), B, H, T, D, dt, plan.q_scale, plan.bound,
+                  plan.vmax, st)
         o = torch.empty_like(q)
         stat = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         precise = plan.low.precise_output or (plan.high is not None and plan.high.precise_output)
         o_precise = torch.empty(q.shape, dtype=torch.float32, device=dev) if precise else None
         lo = _c_variant(plan.low)
         hi = _c_variant(plan.high) if plan.high is not None else None
-        _lib.call("algx_attn_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
-                  _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat), B, H, T, D, dt,
-                  plan.q_scale, lo, hi, _lib.ptr(guard), st)
+        _lib.call("algx_attn_fwd", _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
+                  _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat), B, H, T, D, dt, lo, hi,
+                  _lib.ptr(guard), st)
         ctx.plan = plan
-        ctx.save_for_backward(q, k, v, sink, o, o_precise, stat, guard)
+        ctx.save_for_backward(q_s, k, v, sink, o, o_precise, stat, guard)
         return o
 
     @staticmethod
     def backward(ctx, do):
-        q, k, v, sink, o, o_precise, stat, guard = ctx.saved_tensors
+        q_s, k, v, sink, o, o_precise, stat, guard = ctx.saved_tensors
         plan = ctx.plan
-        B, H, T, D = q.shape
-        dt = _lib.dtype_code(q.dtype)
-        do = do.to(q.dtype).contiguous()
-        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-        dsink = torch.empty((H,), dtype=torch.float32, device=q.device) if sink is not None else None
+        B, H, T, D = q_s.shape
+        dt = _lib.dtype_code(q_s.dtype)
+        do = do.to(q_s.dtype).contiguous()
+        dq, dk, dv = torch.empty_like(q_s), torch.empty_like(k), torch.empty_like(v)
+        dsink = torch.empty((H,), dtype=torch.float32, device=q_s.device) if sink is not None else None
         ws = torch.empty(_lib.query("algx_attn_bwd_workspace_bytes", B, H, T, D),
-                         dtype=torch.uint8, device=q.device)
+                         dtype=torch.uint8, device=q_s.device)
         lo = _c_variant(plan.low)
         hi = _c_variant(plan.high) if plan.high is not None else None
-        _lib.call("algx_attn_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
+        _lib.call("algx_attn_bwd", _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
                   _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat), _lib.ptr(do),
                   _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dsink), _lib.ptr(ws),
                   B, H, T, D, dt, plan.q_scale, lo, hi, _lib.ptr(guard), _lib.stream())

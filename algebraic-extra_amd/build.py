@@ -24,7 +24,8 @@ ARCH = "gfx950"
 # Extra flags per translation unit: the MFMA kernels keep their accumulators in
 # architectural VGPRs so the VALU reads them without accvgpr copies.
 EXTRA = {
-    "attn_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "attn_fwd_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "attn_bwd_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "head.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 

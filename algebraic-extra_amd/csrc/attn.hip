@@ -1,9 +1,10 @@
 // C ABI of the attention kernels: argument validation, variant conversion
 // and dispatch between the MFMA path (bf16, D=64, T%128==0) and the generic
-// path (everything else). Guarded calls enqueue both variants; each kernel
-// reads the device guard word and returns at once when it is not selected,
-// mirroring lax.cond(in_range, low, high) of flash.py:853-856 without a host
-// round trip.
+// path (everything else). A guarded MFMA call launches one kernel that reads
+// the device guard word and runs the low or the high variant for the whole
+// grid; the generic path enqueues both variants and the unselected one
+// returns at once. Either way this mirrors lax.cond(in_range, low, high) of
+// flash.py:853-856 without a host round trip.
 #include <cstdlib>
 
 #include "attn_aux.h"
@@ -50,43 +51,46 @@ using namespace algx;
 
 extern "C" int32_t algx_attn_guard_words(void) { return guard_words(); }
 
-extern "C" int32_t algx_attn_guard(const void* q, const void* k, const void* v, const float* sink,
-                                   int32_t* guard, int32_t B, int32_t H, int32_t T, int32_t D,
-                                   int32_t dtype, float q_scale, float bound, float vmax,
-                                   void* stream) {
+extern "C" int32_t algx_attn_prepare(const void* q, const void* k, const void* v,
+                                     const float* sink, void* q_s, int32_t* guard, int32_t B,
+                                     int32_t H, int32_t T, int32_t D, int32_t dtype,
+                                     float q_scale, float bound, float vmax, void* stream) {
   if (int32_t rc = check_shape(B, H, T, D, dtype)) return rc;
-  if (guard == nullptr) return fail("attn_guard: null guard buffer");
-  if ((int64_t)B * H * T > 0 && (q == nullptr || k == nullptr || v == nullptr))
-    return fail("attn_guard: null input");
-  return launch_guard(q, k, v, sink, guard, B, H, T, D, dtype, q_scale, bound, vmax,
-                      (hipStream_t)stream);
+  if ((int64_t)B * H * T == 0) return 0;
+  if (q == nullptr || q_s == nullptr) return fail("attn_prepare: null q or q_s");
+  if (guard != nullptr && (k == nullptr || v == nullptr))
+    return fail("attn_prepare: the guard needs k and v");
+  return launch_prepare(q, k, v, sink, q_s, guard, B, H, T, D, dtype, q_scale, bound, vmax,
+                        (hipStream_t)stream);
 }
 
 extern "C" int32_t algx_attn_fwd(const void* q, const void* k, const void* v, const float* sink,
                                  void* o, float* o_precise, float* stat, int32_t B, int32_t H,
-                                 int32_t T, int32_t D, int32_t dtype, float q_scale,
+                                 int32_t T, int32_t D, int32_t dtype,
                                  const algx_attn_variant* low, const algx_attn_variant* high,
                                  const int32_t* guard, void* stream) {
   if (int32_t rc = check_shape(B, H, T, D, dtype)) return rc;
   KVariant kl{}, kh{};
   if (int32_t rc = to_kvar(low, kl, "low")) return rc;
-  if (guard != nullptr)
+  if (guard != nullptr) {
     if (int32_t rc = to_kvar(high, kh, "high")) return rc;
+  } else {
+    kh = kl;
+  }
   if ((int64_t)B * H * T == 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || stat == nullptr)
     return fail("attn_fwd: null pointer");
   if ((kl.precise || (guard != nullptr && kh.precise)) && o_precise == nullptr)
     return fail("attn_fwd: precise-output variant needs o_precise");
   hipStream_t s = (hipStream_t)stream;
-  const bool mfma = mfma_supported(T, D, dtype) && !force_generic();
-  auto run = [&](const KVariant& var, int want_low) -> int32_t {
-    return mfma ? launch_fwd_mfma(q, k, v, sink, o, o_precise, stat, B, H, T, q_scale, var,
-                                  guard, want_low, s)
-                : launch_fwd_generic(q, k, v, sink, o, o_precise, stat, B, H, T, D, dtype,
-                                     q_scale, var, guard, want_low, s);
-  };
-  if (int32_t rc = run(kl, 1)) return rc;
-  if (guard != nullptr) return run(kh, 0);
+  if (mfma_supported(T, D, dtype) && !force_generic())
+    return launch_fwd_mfma(q, k, v, sink, o, o_precise, stat, B, H, T, kl, kh, guard, s);
+  if (int32_t rc = launch_fwd_generic(q, k, v, sink, o, o_precise, stat, B, H, T, D, dtype, kl,
+                                      guard, 1, s))
+    return rc;
+  if (guard != nullptr)
+    return launch_fwd_generic(q, k, v, sink, o, o_precise, stat, B, H, T, D, dtype, kh, guard, 0,
+                              s);
   return 0;
 }
 
@@ -129,15 +133,17 @@ extern "C" int32_t algx_attn_bwd(const void* q, const void* k, const void* v, co
   if (int32_t rc = launch_bwd_pre(dout, o, o_precise, stat, sink, di, mfma ? dq_acc : nullptr,
                                   dsink, B, H, T, D, dtype, kl, kh, guard, s))
     return rc;
-  auto run = [&](const KVariant& var, int want_low) -> int32_t {
-    return mfma ? launch_bwd_mfma(q, k, v, stat, di, dout, dq_acc, dk, dv, B, H, T, q_scale, var,
-                                  guard, want_low, s)
-                : launch_bwd_generic(q, k, v, stat, di, dout, dq, dk, dv, B, H, T, D, dtype,
-                                     q_scale, var, guard, want_low, s);
-  };
-  if (int32_t rc = run(kl, 1)) return rc;
+  if (mfma) {
+    if (int32_t rc = launch_bwd_mfma(q, k, v, stat, di, dout, dq_acc, dk, dv, B, H, T, kl, kh,
+                                     guard, s))
+      return rc;
+    return launch_dq_finish(dq_acc, dq, rows * D, dtype, kl, kh, guard, q_scale, s);
+  }
+  if (int32_t rc = launch_bwd_generic(q, k, v, stat, di, dout, dq, dk, dv, B, H, T, D, dtype,
+                                      q_scale, kl, guard, 1, s))
+    return rc;
   if (guard != nullptr)
-    if (int32_t rc = run(kh, 0)) return rc;
-  if (mfma) return launch_dq_finish(dq_acc, dq, rows * D, dtype, kl, kh, guard, q_scale, s);
+    return launch_bwd_generic(q, k, v, stat, di, dout, dq, dk, dv, B, H, T, D, dtype, q_scale, kh,
+                              guard, 0, s);
   return 0;
 }

@@ -6,9 +6,10 @@
 namespace algx {
 
 int32_t guard_words();
-int32_t launch_guard(const void* q, const void* k, const void* v, const float* sink,
-                     int32_t* guard, int B, int H, int T, int D, int dtype, float q_scale,
-                     float bound, float vmax, hipStream_t s);
+// q_s = cast(q * q_scale); with a guard buffer also the range-guard word.
+int32_t launch_prepare(const void* q, const void* k, const void* v, const float* sink, void* q_s,
+                       int32_t* guard, int B, int H, int T, int D, int dtype, float q_scale,
+                       float bound, float vmax, hipStream_t s);
 int32_t launch_bwd_pre(const void* dout, const void* o, const float* o_precise,
                        const float* stat, const float* sink, float* di, float* dq_acc,
                        float* dsink, int B, int H, int T, int D, int dtype, const KVariant& low,
@@ -18,10 +19,10 @@ int32_t launch_dq_finish(const float* acc, void* dq, int64_t n, int dtype, const
                          hipStream_t s);
 
 // Generic kernels: any T, D in {16, 32, 64}, bf16 or f32, every variant.
-int32_t launch_fwd_generic(const void* q, const void* k, const void* v, const float* sink,
+int32_t launch_fwd_generic(const void* q_s, const void* k, const void* v, const float* sink,
                            void* o, float* o_precise, float* stat, int B, int H, int T, int D,
-                           int dtype, float q_scale, const KVariant& var, const int32_t* guard,
-                           int want_low, hipStream_t s);
+                           int dtype, const KVariant& var, const int32_t* guard, int want_low,
+                           hipStream_t s);
 int32_t launch_bwd_generic(const void* q, const void* k, const void* v, const float* stat,
                            const float* di, const void* dout, void* dq, void* dk, void* dv,
                            int B, int H, int T, int D, int dtype, float q_scale,
@@ -30,12 +31,15 @@ int32_t launch_bwd_generic(const void* q, const void* k, const void* v, const fl
 
 // MFMA kernels: bf16, D = 64, T % 128 == 0.
 bool mfma_supported(int T, int D, int dtype);
-int32_t launch_fwd_mfma(const void* q, const void* k, const void* v, const float* sink, void* o,
-                        float* o_precise, float* stat, int B, int H, int T, float q_scale,
-                        const KVariant& var, const int32_t* guard, int want_low, hipStream_t s);
-int32_t launch_bwd_mfma(const void* q, const void* k, const void* v, const float* stat,
+// One launch per call: with a guard word the kernel runs `lo` or `hi` for the
+// whole grid; without one it runs `lo`.
+int32_t launch_fwd_mfma(const void* q_s, const void* k, const void* v, const float* sink,
+                        void* o, float* o_precise, float* stat, int B, int H, int T,
+                        const KVariant& lo, const KVariant& hi, const int32_t* guard,
+                        hipStream_t s);
+int32_t launch_bwd_mfma(const void* q_s, const void* k, const void* v, const float* stat,
                         const float* di, const void* dout, float* dq_acc, void* dk, void* dv,
-                        int B, int H, int T, float q_scale, const KVariant& var,
-                        const int32_t* guard, int want_low, hipStream_t s);
+                        int B, int H, int T, const KVariant& lo, const KVariant& hi,
+                        const int32_t* guard, hipStream_t s);
 
 }  // namespace algx

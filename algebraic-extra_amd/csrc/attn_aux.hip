@@ -23,13 +23,14 @@ template <int LPR> __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
-// One pass over q, k, v: per-block maxima of |q_s|^2 (q_s = cast(q*scale),
-// flash.py:833, :841), |k|^2 (:842) and |v| (:849). NaN becomes +inf so that
-// it fails the guard as jnp.max's NaN does.
+// One pass over q, k, v: writes q_s = cast(q * scale) (flash.py:833) and the
+// per-block maxima of |q_s|^2 (:841), |k|^2 (:842) and |v| (:849). NaN
+// becomes +inf so that it fails the guard as jnp.max's NaN does.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void guard_partial_kernel(const T* __restrict__ q,
+__global__ __launch_bounds__(256) void prepare_guard_kernel(const T* __restrict__ q,
                                                             const T* __restrict__ k,
-                                                            const T* __restrict__ v, int64_t rows,
+                                                            const T* __restrict__ v,
+                                                            T* __restrict__ q_s, int64_t rows,
                                                             float q_scale,
                                                             float* __restrict__ partial) {
   typedef typename V16<T>::type VT;
@@ -46,14 +47,17 @@ __global__ __launch_bounds__(256) void guard_partial_kernel(const T* __restrict_
     VT b = *reinterpret_cast<const VT*>(k + off);
     VT c = *reinterpret_cast<const VT*>(v + off);
     float sq = 0.0f, sk = 0.0f, av = 0.0f;
+    VT qo;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-      const float qs = round_to<T>(to_f(a[i]) * q_scale);
+      qo[i] = from_f<T>(to_f(a[i]) * q_scale);
+      const float qs = to_f(qo[i]);
       sq = __builtin_fmaf(qs, qs, sq);
       const float kk = to_f(b[i]);
       sk = __builtin_fmaf(kk, kk, sk);
       av = __builtin_fmaxf(av, nan_to_inf(__builtin_fabsf(to_f(c[i]))));
     }
+    *reinterpret_cast<VT*>(q_s + off) = qo;
     sq = nan_to_inf(group_sum<LPR>(sq));
     sk = nan_to_inf(group_sum<LPR>(sk));
     mq = __builtin_fmaxf(mq, sq);
@@ -77,6 +81,22 @@ __global__ __launch_bounds__(256) void guard_partial_kernel(const T* __restrict_
     const float* r = red[threadIdx.x];
     partial[(int64_t)blockIdx.x * 3 + threadIdx.x] =
         __builtin_fmaxf(__builtin_fmaxf(r[0], r[1]), __builtin_fmaxf(r[2], r[3]));
+  }
+}
+
+// q_s = cast(q * scale) alone (unguarded calls), flash.py:833.
+template <typename T>
+__global__ __launch_bounds__(256) void scale_kernel(const T* __restrict__ q, T* __restrict__ q_s,
+                                                    int64_t n, float q_scale) {
+  typedef typename V16<T>::type VT;
+  constexpr int EPL = V16<T>::n;
+  int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * EPL;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x * EPL;
+  for (; i < n; i += stride) {
+    VT a = *reinterpret_cast<const VT*>(q + i);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) a[e] = from_f<T>(to_f(a[e]) * q_scale);
+    *reinterpret_cast<VT*>(q_s + i) = a;
   }
 }
 
@@ -208,10 +228,22 @@ constexpr int kGuardBlocks = 1024;
 
 int32_t guard_words() { return 8 + 3 * kGuardBlocks; }
 
-int32_t launch_guard(const void* q, const void* k, const void* v, const float* sink,
-                     int32_t* guard, int B, int H, int T, int D, int dtype, float q_scale,
-                     float bound, float vmax, hipStream_t s) {
+int32_t launch_prepare(const void* q, const void* k, const void* v, const float* sink, void* q_s,
+                       int32_t* guard, int B, int H, int T, int D, int dtype, float q_scale,
+                       float bound, float vmax, hipStream_t s) {
   const int64_t rows = (int64_t)B * H * T;
+  if (guard == nullptr) {
+    const int64_t n = rows * D;
+    const int epl = dtype == ALGX_BF16 ? 8 : 4;
+    int64_t nb = (n / epl + 255) / 256;
+    if (nb > 8192) nb = 8192;
+    if (nb < 1) nb = 1;
+    if (dtype == ALGX_BF16)
+      scale_kernel<bf16><<<(int)nb, 256, 0, s>>>((const bf16*)q, (bf16*)q_s, n, q_scale);
+    else
+      scale_kernel<float><<<(int)nb, 256, 0, s>>>((const float*)q, (float*)q_s, n, q_scale);
+    return check_launch("attn_scale");
+  }
   float* partial = reinterpret_cast<float*>(guard + 8);
   const int epl = dtype == ALGX_BF16 ? 8 : 4;
   const int rpw = 64 / (D / epl);
@@ -219,8 +251,8 @@ int32_t launch_guard(const void* q, const void* k, const void* v, const float* s
   if (nb < 1) nb = 1;
   if (nb > kGuardBlocks) nb = kGuardBlocks;
 #define GUARD_CASE(TT, DD)                                                              \
-  guard_partial_kernel<TT, DD><<<(int)nb, 256, 0, s>>>((const TT*)q, (const TT*)k,      \
-                                                       (const TT*)v, rows, q_scale, partial)
+  prepare_guard_kernel<TT, DD><<<(int)nb, 256, 0, s>>>((const TT*)q, (const TT*)k,      \
+                                                       (const TT*)v, (TT*)q_s, rows, q_scale, partial)
   if (dtype == ALGX_BF16) {
     if (D == 64) GUARD_CASE(bf16, 64);
     else if (D == 32) GUARD_CASE(bf16, 32);

@@ -1,0 +1,305 @@
+// gfx950 MFMA attention forward (flash.py:189-284, head_resident.py:24-93).
+//
+// One workgroup of 4 waves owns 128 queries of one (b, h); each wave owns 32
+// of them and walks 64-key tiles up to the diagonal. The score tile is formed
+// transposed, S^T = K Q_s^T, with v_mfma_f32_32x32x16_bf16 (K from LDS as the
+// A operand, the wave's scaled Q rows in registers as the B operand), so each
+// lane holds 16 keys of ONE query row. The asinh/softmax weight, the causal
+// mask and the row sum run on those registers; the bf16 weights go straight
+// back as the B operand of O^T += V^T P^T, whose A operand is a V^T tile in
+// LDS written with the k-slot order the accumulator layout implies.
+//
+// Software pipeline: the score MFMAs of tile j+1 are issued before the VALU
+// transform of tile j, so the MFMA pipe works while the VALU (the bound of
+// this kernel: about eight VALU operations and one reciprocal square root per
+// score against 256 MFMA flops) runs. K therefore lives one tile ahead of V
+// in a two-buffer LDS ring: iteration j reads K_{j+1} and V_j and fills
+// K_{j+2} and V_{j+1}.
+#include <type_traits>
+
+#include "attn_mfma.h"
+
+namespace algx {
+namespace mfma {
+namespace {
+
+template <int MODE, bool FAST, bool BOUNDED, int L2N>
+__device__ __forceinline__ void fwd_body(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
+    float* __restrict__ stat, int H, int T_, const KVariant& var, bf16 (*Ks)[FBN * KSTR],
+    bf16 (*Vt)[HD * VSTR]) {
+  const int nheads = gridDim.x / (T_ / FBM);
+  int bh, qb;
+  map_block(blockIdx.x, nheads, T_ / FBM, true, bh, qb);
+  const int h = bh % H;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
+  const int64_t base = (int64_t)bh * T_ * HD;
+  const int q0 = qb * FBM, qw = q0 + 32 * w, qrow = qw + c32;
+  const int log2n = var.log2n;
+
+  // B operand of S^T = K Q_s^T: lane holds Q_s[qrow][16*ks + 8*g .. +7].
+  bf16x8 qreg[4];
+  {
+    const bf16* qp = q + base + (int64_t)qrow * HD + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qreg[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks);
+  }
+
+  const bool has_sink = sink != nullptr;
+  float m_row, l_row;
+  sink_init(var, has_sink, has_sink ? sink[h] : 0.0f, m_row, l_row);
+  if (g == 1) l_row = 0.0f;  // the two lane halves carry partial row sums
+  f32x16 oacc[2];
+  zero16(oacc[0]);
+  zero16(oacc[1]);
+
+  // Loaders: threads 0..127 move K tiles (row-major), 128..255 move V tiles
+  // (4 keys x 8 d each, transposed into V^T on the LDS store).
+  bf16x8 pre[4];
+  const bool kloader = tid < 128;
+  const int u = tid & 127;
+  const int nkb = (q0 + FBM) / FBN;
+  auto gload = [&](int kb) {
+    const bf16* src = (kloader ? k : v) + base + (int64_t)kb * FBN * HD;
+    if (kloader) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int id = u + 128 * c;
+        pre[c] = *reinterpret_cast<const bf16x8*>(src + (id >> 3) * HD + (id & 7) * 8);
+      }
+    } else {
+      const int kg = u >> 3, dc = u & 7;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        pre[i] = *reinterpret_cast<const bf16x8*>(src + (4 * kg + i) * HD + 8 * dc);
+    }
+  };
+  auto lstore = [&](int buf) {
+    if (kloader) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int id = u + 128 * c;
+        *reinterpret_cast<bf16x8*>(&Ks[buf][(id >> 3) * KSTR + (id & 7) * 8]) = pre[c];
+      }
+    } else {
+      const int kg = u >> 3, dc = u & 7;
+      const int pos = 16 * (kg >> 2) + slot_pos(4 * (kg & 3));
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        bf16x4 col = {pre[0][d], pre[1][d], pre[2][d], pre[3][d]};
+        *reinterpret_cast<bf16x4*>(&Vt[buf][(8 * dc + d) * VSTR + pos]) = col;
+      }
+    }
+  };
+  // Tile each loader group fetches in iteration kb (K two ahead, V one ahead).
+  auto my_tile = [&](int kb) { return kloader ? kb + 2 : kb + 1; };
+
+  // Prologue: K_0, K_1 and V_0 in LDS; K_2 / V_1 in flight.
+  if (kloader) {
+    gload(0);
+    lstore(0);
+    if (nkb > 1) {
+      gload(1);
+      lstore(1);
+    }
+  } else {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  if (my_tile(0) < nkb) gload(my_tile(0));
+
+  auto scores = [&](int kb, f32x16 (&s)[2]) {
+    const int buf = kb & 1;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      zero16(s[mt]);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 a =
+            *reinterpret_cast<const bf16x8*>(&Ks[buf][(32 * mt + c32) * KSTR + 16 * ks + 8 * g]);
+        s[mt] = mfma32(a, qreg[ks], s[mt]);
+      }
+    }
+  };
+
+  // Transform tile kb's scores (cur) into weights, accumulate P V. Only tiles
+  // that cross the diagonal (diag_tag = true_type) evaluate the causal mask.
+  auto consume = [&](auto diag_tag, int kb, f32x16 (&cur)[2]) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    const int k0 = kb * FBN;
+    float lsum = 0.0f;
+    if (MODE == MODE_NOSHIFT) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float s = cur[mt][r];
+          const float x = BOUNDED ? s : __builtin_fminf(s, var.clamp);
+          float rr;
+          float p = powN<L2N>(FAST ? rho_fast(x, rr) : rho_exact(x, rr), log2n);
+          if (DIAG && k0 + 32 * mt + 8 * (r >> 2) + 4 * g + (r & 3) > qrow) p = 0.0f;
+          cur[mt][r] = p;
+          lsum += p;
+        }
+      l_row += lsum;
+    } else {
+      float tmax = -__builtin_inff();
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float s = cur[mt][r];
+          if (DIAG && k0 + 32 * mt + 8 * (r >> 2) + 4 * g + (r & 3) > qrow) s = -__builtin_inff();
+          cur[mt][r] = s;
+          tmax = __builtin_fmaxf(tmax, s);
+        }
+      tmax = __builtin_fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      float m_new = __builtin_fmaxf(m_row, tmax), m_prev = m_row;
+      if (!has_sink && kb == 0) {  // flash.py:239-245
+        m_new = tmax;
+        m_prev = m_new;
+      }
+      float alpha;
+      if (MODE == MODE_SOFTMAX) {
+        alpha = __builtin_amdgcn_exp2f((m_prev - m_new) * kLog2e);
+        const float mb = m_new * kLog2e;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[mt][r], kLog2e, -mb));
+            cur[mt][r] = p;
+            lsum += p;
+          }
+      } else {
+        float rr;
+        const float shf = rho_exact(-m_new, rr);
+        alpha = powN<L2N>(rho_exact(m_prev, rr) * shf, log2n);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float s = cur[mt][r];
+            float p = powN<L2N>((FAST ? rho_fast(s, rr) : rho_exact(s, rr)) * shf, log2n);
+            if (s == -__builtin_inff()) p = 0.0f;
+            cur[mt][r] = p;
+            lsum += p;
+          }
+      }
+      l_row = __builtin_fmaf(l_row, alpha, lsum);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+      m_row = m_new;
+    }
+    // O^T += V^T P^T over four 16-key chunks.
+    const int buf = kb & 1;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      const int mt = kc >> 1, rr = 8 * (kc & 1);
+      bf16x8 pb;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) pb[s] = (bf16)cur[mt][rr + s];
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const bf16x8 a =
+            *reinterpret_cast<const bf16x8*>(&Vt[buf][(32 * dt + c32) * VSTR + 16 * kc + 8 * g]);
+        oacc[dt] = mfma32(a, pb, oacc[dt]);
+      }
+    }
+  };
+
+  auto visible = [&](int kb) { return kb < nkb && kb * FBN <= qw + 31; };
+  auto step = [&](int kb, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+    if (visible(kb + 1)) scores(kb + 1, nxt);
+    if (visible(kb)) {
+      if (kb * FBN + FBN - 1 > qw)
+        consume(std::true_type{}, kb, cur);
+      else
+        consume(std::false_type{}, kb, cur);
+    }
+    const int t = my_tile(kb);
+    if (t < nkb) lstore(kloader ? (kb & 1) : ((kb + 1) & 1));
+    __syncthreads();
+    if (my_tile(kb + 1) < nkb) gload(my_tile(kb + 1));
+  };
+
+  f32x16 sa[2], sb[2];
+  scores(0, sa);
+  // Step 0 refills K buffer 0 (K_2): every wave must have read K_0 first.
+  // Later steps refill a K buffer read one step earlier, before that step's
+  // closing barrier.
+  __syncthreads();
+  for (int kb = 0; kb < nkb; kb += 2) {
+    step(kb, sa, sb);
+    if (kb + 1 < nkb) step(kb + 1, sb, sa);
+  }
+
+  const float l_tot = l_row + __shfl_xor(l_row, 32, 64);
+  const float inv = 1.0f / l_tot;
+  const int64_t orow = base + (int64_t)qrow * HD;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 32 * dt + 8 * j + 4 * g;
+      f32x4 val;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) val[i] = oacc[dt][4 * j + i] * inv;
+      bf16x4 ob = {(bf16)val[0], (bf16)val[1], (bf16)val[2], (bf16)val[3]};
+      *reinterpret_cast<bf16x4*>(o + orow + d) = ob;
+      if (MODE == MODE_SHIFT && var.precise && o_precise != nullptr)
+        *reinterpret_cast<f32x4*>(o_precise + orow + d) = val;
+    }
+  if (g == 0) stat[(int64_t)bh * T_ + qrow] = final_stat(var, m_row, l_tot);
+}
+
+// One launch per call: the guard word (if any) picks the low or the high
+// variant for the whole grid, mirroring lax.cond(in_range, low, high).
+template <int LO, int HI>
+__global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
+    float* __restrict__ stat, int H, int T_, KVariant lo, KVariant hi,
+    const int32_t* __restrict__ guard) {
+  __shared__ __attribute__((aligned(16))) bf16 Ks[2][FBN * KSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Vt[2][HD * VSTR];
+  if (LO == HI || guard_in_range(guard))
+    fwd_body<LO & 3, (LO & 4) != 0, (LO & 8) != 0, (LO >> 4)>(q, k, v, sink, o, o_precise, stat,
+                                                              H, T_, lo, Ks, Vt);
+  else
+    fwd_body<HI & 3, (HI & 4) != 0, (HI & 8) != 0, (HI >> 4)>(q, k, v, sink, o, o_precise, stat,
+                                                              H, T_, hi, Ks, Vt);
+}
+
+typedef void (*FwdFn)(const bf16*, const bf16*, const bf16*, const float*, bf16*, float*, float*,
+                      int, int, KVariant, KVariant, const int32_t*);
+
+FwdFn pick_fwd(int cl, int ch) { ALGX_PICK_ALL(fwd_mfma_kernel) }
+
+}  // namespace
+}  // namespace mfma
+
+bool mfma_supported(int T, int D, int dtype) {
+  return dtype == ALGX_BF16 && D == mfma::HD && T >= mfma::FBM && T % mfma::FBM == 0 &&
+         T % mfma::BBN == 0;
+}
+
+int32_t launch_fwd_mfma(const void* q, const void* k, const void* v, const float* sink, void* o,
+                        float* o_precise, float* stat, int B, int H, int T, const KVariant& lo,
+                        const KVariant& hi, const int32_t* guard, hipStream_t s) {
+  using namespace mfma;
+  const int grid = B * H * (T / FBM);
+  FwdFn fn = pick_fwd(cfg_for(lo), guard != nullptr ? cfg_for(hi) : cfg_for(lo));
+  if (fn == nullptr) return fail("attn_fwd: no MFMA kernel for this variant pair");
+  ProbeScope probe(ALGX_PROBE_ATTN_FWD, s);
+  fn<<<grid, 256, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)v, sink, (bf16*)o,
+                          o_precise, stat, H, T, lo, hi, guard);
+  return check_launch("attn_fwd_mfma");
+}
+
+}  // namespace algx

@@ -19,8 +19,8 @@ template <typename T, int D>
 __global__ __launch_bounds__(kTile) void fwd_generic_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ sink, T* __restrict__ o, float* __restrict__ o_precise,
-    float* __restrict__ stat, int H, int T_, float q_scale, KVariant var,
-    const int32_t* __restrict__ guard, int want_low) {
+    float* __restrict__ stat, int H, int T_, KVariant var, const int32_t* __restrict__ guard,
+    int want_low) {
   if (guard != nullptr && (int)guard_in_range(guard) != want_low) return;
   const int bh = blockIdx.y, h = bh % H, t = threadIdx.x;
   const int i = blockIdx.x * kTile + t;
@@ -31,7 +31,7 @@ __global__ __launch_bounds__(kTile) void fwd_generic_kernel(
   float qr[D], acc[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    qr[d] = valid ? round_to<T>(to_f(q[base + (int64_t)i * D + d]) * q_scale) : 0.0f;
+    qr[d] = valid ? to_f(q[base + (int64_t)i * D + d]) : 0.0f;
     acc[d] = 0.0f;
   }
   const bool has_sink = sink != nullptr;
@@ -121,7 +121,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(kTile) void bwd_dkdv_generic_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const float* __restrict__ stat, const float* __restrict__ di, const T* __restrict__ dout,
-    T* __restrict__ dk, T* __restrict__ dv, int T_, float q_scale, KVariant var,
+    T* __restrict__ dk, T* __restrict__ dv, int T_, KVariant var,
     const int32_t* __restrict__ guard, int want_low) {
   if (guard != nullptr && (int)guard_in_range(guard) != want_low) return;
   const int bh = blockIdx.y, t = threadIdx.x;
@@ -147,7 +147,7 @@ __global__ __launch_bounds__(kTile) void bwd_dkdv_generic_kernel(
     const int i = qt * kTile + t;
 #pragma unroll 8
     for (int d = 0; d < D; ++d) {
-      Qs[t][d] = i < T_ ? round_to<T>(to_f(q[base + (int64_t)i * D + d]) * q_scale) : 0.0f;
+      Qs[t][d] = i < T_ ? to_f(q[base + (int64_t)i * D + d]) : 0.0f;
       Gs[t][d] = i < T_ ? to_f(dout[base + (int64_t)i * D + d]) : 0.0f;
     }
     Ss[t] = i < T_ ? stat[(int64_t)bh * T_ + i] : 0.0f;
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kTile) void bwd_dq_generic_kernel(
   float qr[D], gr[D], dqa[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    qr[d] = valid ? round_to<T>(to_f(q[base + (int64_t)i * D + d]) * q_scale) : 0.0f;
+    qr[d] = valid ? to_f(q[base + (int64_t)i * D + d]) : 0.0f;
     gr[d] = valid ? to_f(dout[base + (int64_t)i * D + d]) : 0.0f;
     dqa[d] = 0.0f;
   }
@@ -250,13 +250,13 @@ __global__ __launch_bounds__(kTile) void bwd_dq_generic_kernel(
 
 int32_t launch_fwd_generic(const void* q, const void* k, const void* v, const float* sink,
                            void* o, float* o_precise, float* stat, int B, int H, int T, int D,
-                           int dtype, float q_scale, const KVariant& var, const int32_t* guard,
-                           int want_low, hipStream_t s) {
+                           int dtype, const KVariant& var, const int32_t* guard, int want_low,
+                           hipStream_t s) {
   dim3 grid((T + kTile - 1) / kTile, B * H);
 #define FWD_CASE(TT, DD)                                                                      \
   fwd_generic_kernel<TT, DD><<<grid, kTile, 0, s>>>((const TT*)q, (const TT*)k, (const TT*)v, \
-                                                    sink, (TT*)o, o_precise, stat, H, T,      \
-                                                    q_scale, var, guard, want_low)
+                                                    sink, (TT*)o, o_precise, stat, H, T, var, \
+                                                    guard, want_low)
   if (dtype == ALGX_BF16) {
     if (D == 64) FWD_CASE(bf16, 64);
     else if (D == 32) FWD_CASE(bf16, 32);
@@ -282,7 +282,7 @@ int32_t launch_bwd_generic(const void* q, const void* k, const void* v, const fl
   do {                                                                                          \
     bwd_dkdv_generic_kernel<TT, DD><<<grid, kTile, 0, s>>>(                                     \
         (const TT*)q, (const TT*)k, (const TT*)v, stat, di, (const TT*)dout, (TT*)dk, (TT*)dv, \
-        T, q_scale, var, guard, want_low);                                                      \
+        T, var, guard, want_low);                                                               \
     bwd_dq_generic_kernel<TT, DD><<<grid, kTile, 0, s>>>((const TT*)q, (const TT*)k,            \
                                                          (const TT*)v, stat, di,                \
                                                          (const TT*)dout, (TT*)dq, T, q_scale,  \

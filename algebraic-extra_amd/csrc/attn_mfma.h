@@ -1,0 +1,121 @@
+// Shared pieces of the gfx950 MFMA attention kernels (bf16, D = 64).
+#pragma once
+
+#include "attn_aux.h"
+
+namespace algx {
+namespace mfma {
+
+constexpr int HD = 64;
+// forward tiles: 128 queries per workgroup (32 per wave), 64-key tiles
+constexpr int FBM = 128, FBN = 64;
+constexpr int KSTR = 72;  // K tile row stride (bf16): 144 B rows
+constexpr int VSTR = 72;  // V^T tile row stride
+// backward tiles: 128 keys per workgroup (32 per wave), 64-query tiles
+constexpr int BBN = 128, BBM = 64;
+constexpr int QSTR = 72;    // Q_s / dO row stride (64 d)
+constexpr int QTSTR = 72;   // Q_s^T / dO^T row stride (64 q)
+constexpr int DSSTR = 136;  // dS row stride (128 keys)
+constexpr int KTSTR = 136;  // K^T row stride (128 keys)
+
+enum { MODE_SOFTMAX = 0, MODE_NOSHIFT = 1, MODE_SHIFT = 2 };
+
+// Kernel configuration packed in one int: MODE | FAST << 2 | BOUNDED << 3 | L2N << 4.
+constexpr int cfg_of(int mode, bool fast, bool bounded, int l2n) {
+  return mode | (fast ? 4 : 0) | (bounded ? 8 : 0) | (l2n << 4);
+}
+// Power template argument: n = 8, 16, 32 unrolled; other n by a runtime loop.
+inline int l2n_arg(int log2n) { return (log2n >= 3 && log2n <= 5) ? log2n : 0; }
+inline int cfg_for(const KVariant& v) {
+  if (v.kind == ALGX_SOFTMAX) return cfg_of(MODE_SOFTMAX, false, false, 1);
+  if (v.shift) return cfg_of(MODE_SHIFT, v.fast != 0, false, l2n_arg(v.log2n));
+  return cfg_of(MODE_NOSHIFT, v.fast != 0, v.bounded != 0, l2n_arg(v.log2n));
+}
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void zero16(f32x16& a) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) a[r] = 0.0f;
+}
+
+// Position of key (or query) offset `off` (0..15) inside a 16-wide chunk of
+// a transposed operand tile: bits 2 and 3 swapped, i.e. k-slot (g, s) of
+// lane group g holds offset 8*(s/4) + 4*g + s%4, which is exactly the set of
+// rows a 32x32 accumulator lane holds in registers 8*(j%2)..+7 of chunk j.
+__device__ __forceinline__ int slot_pos(int off) {
+  return (off & 3) | ((off >> 3) & 1) << 2 | ((off >> 2) & 1) << 3;
+}
+
+// blockIdx -> (head, tile): heads are dealt to XCDs (blockIdx % 8) so every
+// tile of a head runs on the same XCD and shares its L2; tiles are issued in
+// order of decreasing causal work when `descending`.
+__device__ __forceinline__ void map_block(int bid, int nheads, int ntiles, bool descending,
+                                          int& bh, int& tile) {
+  int r;
+  if ((nheads & 7) == 0) {
+    const int nh8 = nheads >> 3;
+    r = bid >> 3;
+    bh = (bid & 7) + 8 * (r % nh8);
+    r = r / nh8;
+  } else {
+    bh = bid % nheads;
+    r = bid / nheads;
+  }
+  tile = descending ? ntiles - 1 - r : r;
+}
+
+__device__ __forceinline__ bf16x8 scale_bf16x8(bf16x8 x, float s) {
+  bf16x8 y;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = (bf16)((float)x[e] * s);
+  return y;
+}
+
+// x^(2^log2n) with a compile-time exponent when L2N > 0 (int_pow of flash.py:95-104).
+template <int L2N> __device__ __forceinline__ float powN(float x, int log2n) {
+  if (L2N > 0) {
+#pragma unroll
+    for (int i = 0; i < L2N; ++i) x = x * x;
+    return x;
+  }
+  return pow2n(x, log2n);
+}
+
+}  // namespace mfma
+}  // namespace algx
+
+// Every asinh configuration instantiated as a single-variant kernel.
+#define ALGX_ASINH_CFGS(X, K)                                                          \
+  X(K, cfg_of(MODE_SHIFT, true, false, 3)) X(K, cfg_of(MODE_SHIFT, true, false, 4))    \
+  X(K, cfg_of(MODE_SHIFT, true, false, 5)) X(K, cfg_of(MODE_SHIFT, true, false, 0))    \
+  X(K, cfg_of(MODE_SHIFT, false, false, 3)) X(K, cfg_of(MODE_SHIFT, false, false, 4))  \
+  X(K, cfg_of(MODE_SHIFT, false, false, 5)) X(K, cfg_of(MODE_SHIFT, false, false, 0))  \
+  X(K, cfg_of(MODE_NOSHIFT, true, true, 3)) X(K, cfg_of(MODE_NOSHIFT, true, true, 4))  \
+  X(K, cfg_of(MODE_NOSHIFT, true, true, 5)) X(K, cfg_of(MODE_NOSHIFT, true, true, 0))  \
+  X(K, cfg_of(MODE_NOSHIFT, false, true, 3)) X(K, cfg_of(MODE_NOSHIFT, false, true, 4)) \
+  X(K, cfg_of(MODE_NOSHIFT, false, true, 5)) X(K, cfg_of(MODE_NOSHIFT, false, true, 0)) \
+  X(K, cfg_of(MODE_NOSHIFT, true, false, 3)) X(K, cfg_of(MODE_NOSHIFT, true, false, 4)) \
+  X(K, cfg_of(MODE_NOSHIFT, true, false, 5)) X(K, cfg_of(MODE_NOSHIFT, true, false, 0)) \
+  X(K, cfg_of(MODE_NOSHIFT, false, false, 3)) X(K, cfg_of(MODE_NOSHIFT, false, false, 4)) \
+  X(K, cfg_of(MODE_NOSHIFT, false, false, 5)) X(K, cfg_of(MODE_NOSHIFT, false, false, 0))
+
+#define ALGX_PICK_SINGLE(K, C) \
+  if (cl == (C)) return K<(C), (C)>;
+// Guarded launches pair a bounded unshifted low variant with the shifted
+// exact-rho high variant of the same n (flash.py:850-852).
+#define ALGX_PICK_GUARDED(K, FASTLO, L2)                                                    \
+  if (cl == cfg_of(MODE_NOSHIFT, FASTLO, true, L2) && ch == cfg_of(MODE_SHIFT, false, false, L2)) \
+    return K<cfg_of(MODE_NOSHIFT, FASTLO, true, L2), cfg_of(MODE_SHIFT, false, false, L2)>;
+#define ALGX_PICK_ALL(K)                                                                 \
+  if (cl == ch) {                                                                        \
+    ALGX_PICK_SINGLE(K, cfg_of(MODE_SOFTMAX, false, false, 1))                           \
+    ALGX_ASINH_CFGS(ALGX_PICK_SINGLE, K)                                                 \
+    return nullptr;                                                                      \
+  }                                                                                      \
+  ALGX_PICK_GUARDED(K, true, 3) ALGX_PICK_GUARDED(K, true, 4) ALGX_PICK_GUARDED(K, true, 5) \
+  ALGX_PICK_GUARDED(K, true, 0) ALGX_PICK_GUARDED(K, false, 3) ALGX_PICK_GUARDED(K, false, 4) \
+  ALGX_PICK_GUARDED(K, false, 5) ALGX_PICK_GUARDED(K, false, 0)                          \
+  return nullptr;

@@ -25,6 +25,20 @@ int32_t check_launch(const char* what);
 // Fills n floats on stream s with a kernel (no memset node).
 int32_t fill_f32(float* p, int64_t n, float value, hipStream_t s);
 
+// Records the registered probe events around one kernel launch (see
+// algx_set_probe): construct just before the launch, destroy just after.
+class ProbeScope {
+ public:
+  ProbeScope(int which, hipStream_t s);
+  ~ProbeScope();
+  ProbeScope(const ProbeScope&) = delete;
+  ProbeScope& operator=(const ProbeScope&) = delete;
+
+ private:
+  bool active_;
+  hipStream_t stream_;
+};
+
 // ------------------------------------------------------------- scalar math
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(bf16 x) { return (float)x; }

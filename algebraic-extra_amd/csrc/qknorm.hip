@@ -7,7 +7,8 @@
 // Single pass over HBM: each row is split over LPR lanes that each move one
 // 16-byte vector (8 bf16 or 4 f32); the row sum of squares is combined with
 // xor-shuffles inside the LPR-lane group. dgain is reduced per block into a
-// workspace row and summed by a one-block finishing kernel (deterministic).
+// workspace row and summed by a finishing kernel with one block per column
+// (deterministic).
 #include "common.h"
 
 namespace algx {
@@ -127,14 +128,26 @@ __global__ __launch_bounds__(kThreads) void qknorm_bwd_kernel(
 __global__ __launch_bounds__(kThreads) void qknorm_gain_finish(const float* __restrict__ partial,
                                                                int nblocks,
                                                                float* __restrict__ dgain) {
-  // 256 threads: 4 slices of the block list per column.
-  __shared__ float red[4][kD];
-  const int col = threadIdx.x % kD, slice = threadIdx.x / kD;
-  float s = 0.0f;
-  for (int b = slice; b < nblocks; b += 4) s += partial[(int64_t)b * kD + col];
-  red[slice][col] = s;
+  // One block per gain column: every thread sums a strided slice of the block
+  // partials with independent loads in flight, then a fixed-order tree in LDS
+  // finishes the column (deterministic for a given grid).
+  __shared__ float red[kThreads];
+  const int col = blockIdx.x;
+  float s0 = 0.0f, s1 = 0.0f;
+  int b = threadIdx.x;
+  for (; b + kThreads < nblocks; b += 2 * kThreads) {
+    s0 += partial[(int64_t)b * kD + col];
+    s1 += partial[(int64_t)(b + kThreads) * kD + col];
+  }
+  if (b < nblocks) s0 += partial[(int64_t)b * kD + col];
+  red[threadIdx.x] = s0 + s1;
   __syncthreads();
-  if (threadIdx.x < kD) dgain[col] = red[0][col] + red[1][col] + red[2][col] + red[3][col];
+#pragma unroll
+  for (int w = kThreads / 2; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) dgain[col] = red[0];
 }
 
 int blocks_for(int64_t rows, int dtype) {
@@ -169,6 +182,7 @@ extern "C" int32_t algx_qknorm_fwd(const void* x, const float* gain, void* y, in
   if (y == nullptr) return fail("qknorm: null output");
   hipStream_t s = (hipStream_t)stream;
   const int nb = blocks_for(rows, dtype);
+  ProbeScope probe(ALGX_PROBE_QKNORM_FWD, s);
   if (dtype == ALGX_BF16)
     qknorm_fwd_kernel<bf16><<<nb, kThreads, 0, s>>>((const bf16*)x, gain, (bf16*)y, rows, eps);
   else
@@ -193,13 +207,16 @@ extern "C" int32_t algx_qknorm_bwd(const void* x, const float* gain, const void*
   if (dy == nullptr || dx == nullptr) return fail("qknorm: null dy/dx");
   const int nb = blocks_for(rows, dtype);
   float* partial = (float*)workspace;
-  if (dtype == ALGX_BF16)
-    qknorm_bwd_kernel<bf16><<<nb, kThreads, 0, s>>>((const bf16*)x, gain, (const bf16*)dy,
-                                                    (bf16*)dx, partial, rows, eps);
-  else
-    qknorm_bwd_kernel<float><<<nb, kThreads, 0, s>>>((const float*)x, gain, (const float*)dy,
-                                                     (float*)dx, partial, rows, eps);
+  {
+    ProbeScope probe(ALGX_PROBE_QKNORM_BWD, s);
+    if (dtype == ALGX_BF16)
+      qknorm_bwd_kernel<bf16><<<nb, kThreads, 0, s>>>((const bf16*)x, gain, (const bf16*)dy,
+                                                      (bf16*)dx, partial, rows, eps);
+    else
+      qknorm_bwd_kernel<float><<<nb, kThreads, 0, s>>>((const float*)x, gain, (const float*)dy,
+                                                       (float*)dx, partial, rows, eps);
+  }
   if (int32_t rc = check_launch("qknorm_bwd")) return rc;
-  qknorm_gain_finish<<<1, kThreads, 0, s>>>(partial, nb, dgain);
+  qknorm_gain_finish<<<kD, kThreads, 0, s>>>(partial, nb, dgain);
   return check_launch("qknorm_gain_finish");
 }

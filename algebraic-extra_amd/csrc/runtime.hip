@@ -1,10 +1,34 @@
 // Error reporting and small utility kernels shared by the algx entry points.
+#include <mutex>
+
 #include "common.h"
 
 namespace algx {
 
 namespace {
 thread_local std::string g_error;
+// Process-wide: frameworks launch backward passes from their own threads.
+struct Probe {
+  int which = ALGX_PROBE_NONE;
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+std::mutex g_probe_mu;
+Probe g_probe;
+}  // namespace
+
+ProbeScope::ProbeScope(int which, hipStream_t s) : active_(false), stream_(s) {
+  std::lock_guard<std::mutex> lk(g_probe_mu);
+  if (g_probe.which != ALGX_PROBE_NONE && g_probe.which == which) {
+    active_ = true;
+    hipEventRecord(g_probe.start, stream_);
+  }
+}
+
+ProbeScope::~ProbeScope() {
+  if (!active_) return;
+  std::lock_guard<std::mutex> lk(g_probe_mu);
+  hipEventRecord(g_probe.stop, stream_);
 }
 
 void set_error(const std::string& msg) { g_error = msg; }
@@ -61,6 +85,16 @@ extern "C" int32_t algx_selftest_mfma32(const void* a, const void* bt, float* d,
   algx::selftest_mfma32_kernel<<<1, 64, 0, (hipStream_t)stream>>>((const algx::bf16*)a,
                                                                  (const algx::bf16*)bt, d);
   return algx::check_launch("selftest_mfma32");
+}
+
+extern "C" int32_t algx_set_probe(int32_t which, void* start_event, void* stop_event) {
+  if (which != ALGX_PROBE_NONE && (start_event == nullptr || stop_event == nullptr))
+    return algx::fail("set_probe: null event");
+  std::lock_guard<std::mutex> lk(algx::g_probe_mu);
+  algx::g_probe.which = which;
+  algx::g_probe.start = (hipEvent_t)start_event;
+  algx::g_probe.stop = (hipEvent_t)stop_event;
+  return 0;
 }
 
 extern "C" const char* algx_last_error(void) { return algx::g_error.c_str(); }

@@ -1,0 +1,282 @@
+#!/usr/bin/env python3
+"""Benchmark of the algebraic-extra hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+
+A step is one forward+backward of the guarded asinh-power causal attention
+(flash_attention(kind="asinh", n=16, c=8, range_guard=True), the model's
+call, model.py:145-150) at BASELINE.json configs[1]: B=8, H=12, T=2048,
+D=64, bf16, q/k QK-normalised N(0,1), v and dO N(0,1), synthetic and seeded.
+`value` is that step's throughput in TFLOP/s under the reference's FLOP
+convention (bench_attention.py:50,65: fwd+bwd = 3.5 * 4*B*H*T^2*D/2).
+
+One JSON line is printed. Besides the contract keys it carries:
+  roofline      the dominant kernel (attention backward) timed with HIP events
+                recorded around its launch on its own stream, against the
+                MI355X dense bf16 MFMA peak;
+  cpu_baseline  the reference's dense algebraic attention restated in torch
+                CPU float32 (oracle/cpu_baseline.py) on a bounded sample;
+  secondary     configs[3] attention (H=16), the fused LM head + loss at
+                configs[2] (tokens/s, TFLOP/s by bench_head.py:36) and the
+                QK RMS-norm kernels at configs[3] (GB/s against 8 TB/s).
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "algebraic-extra_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "asinh-attn fwd+bwd TFLOP/s (S=2048,D=64 bf16); fused-head tokens/s; %roofline"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (no sparsity)
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def attn_flops_fwd(B, H, T, D):
+    return 4.0 * B * H * T * T * D / 2.0      # causal, bench_attention.py:50
+
+
+def make_attention_inputs(B, H, T, D, seed, dev):
+    import torch
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn((B, H, T, D), device=dev, generator=gen)
+    k = torch.randn((B, H, T, D), device=dev, generator=gen)
+    q = (q * torch.rsqrt((q * q).mean(-1, keepdim=True) + 1e-5)).bfloat16()
+    k = (k * torch.rsqrt((k * k).mean(-1, keepdim=True) + 1e-5)).bfloat16()
+    v = torch.randn((B, H, T, D), device=dev, generator=gen).bfloat16()
+    do = torch.randn((B, H, T, D), device=dev, generator=gen).bfloat16()
+    return [x.requires_grad_(True) for x in (q, k, v)] + [do]
+
+
+class Probe:
+    """HIP events recorded by libalgx around one named kernel (algx_set_probe)."""
+
+    def __init__(self, which, count):
+        import torch
+        from algebraic_amd import _lib
+        self._lib = _lib
+        self.which = _lib.PROBE[which]
+        self.pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                      for _ in range(count)]
+        for a, b in self.pairs:          # materialise the underlying hipEvents
+            a.record()
+            b.record()
+        torch.cuda.synchronize()
+
+    def arm(self, i):
+        a, b = self.pairs[i]
+        self._lib.call("algx_set_probe", self.which, a.cuda_event, b.cuda_event)
+
+    def disarm(self):
+        self._lib.call("algx_set_probe", 0, None, None)
+
+    def mean_ms(self, count=None):
+        pairs = self.pairs[:count] if count else self.pairs
+        return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
+
+
+def time_steps(step, steps, warmup, probe=None):
+    """Wall time per step over `steps` after `warmup`; probe armed per step."""
+    import torch
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        if probe is not None:
+            probe.arm(i)
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    if probe is not None:
+        probe.disarm()
+    return dt
+
+
+def bench_attention(B, H, T, D, steps, warmup, dev):
+    import torch
+    from algebraic_amd.kernels import flash_attention
+    q, k, v, do = make_attention_inputs(B, H, T, D, 1, dev)
+    kw = dict(kind="asinh", n=16, c=8.0, range_guard=True)
+
+    def step():
+        o = flash_attention(q, k, v, **kw)
+        torch.autograd.grad(o, (q, k, v), do)
+
+    bwd_probe = Probe("attn_bwd", steps)
+    dt = time_steps(step, steps, warmup, bwd_probe)
+    fwd_probe = Probe("attn_fwd", steps)
+    time_steps(step, steps, 1, fwd_probe)
+    f_fwd = attn_flops_fwd(B, H, T, D)
+    return {
+        "ms_per_step": dt * 1e3,
+        "tflops": 3.5 * f_fwd / dt / 1e12,
+        "bwd_kernel_ms": bwd_probe.mean_ms(),
+        "fwd_kernel_ms": fwd_probe.mean_ms(),
+        "bwd_flops": 2.5 * f_fwd,
+        "fwd_flops": f_fwd,
+    }
+
+
+def bench_head(steps, warmup, dev, N=16384, d=768, V=50304, kind="alg_ce", n=8, c=2.0):
+    import torch
+    from algebraic_amd.kernels import fused_head
+    gen = torch.Generator(device=dev).manual_seed(2)
+    h = torch.randn((N, d), device=dev, generator=gen).bfloat16().requires_grad_(True)
+    E = (torch.randn((V, d), device=dev, generator=gen) * 0.02).bfloat16().requires_grad_(True)
+    t = torch.randint(0, V, (N,), device=dev, generator=gen, dtype=torch.int64)
+
+    def step():
+        obj, _ = fused_head(h, E, t, kind=kind, n=n, c=c)
+        torch.autograd.grad(obj, (h, E))
+
+    dt = time_steps(step, steps, warmup)
+    flops = 3 * 2 * N * d * V
+    return {"workload": f"N={N},d={d},V={V},{kind} n={n} c={c}", "ms_per_step": dt * 1e3,
+            "tokens_per_s": N / dt, "tflops": flops / dt / 1e12,
+            "frac": flops / dt / 1e12 / PEAK_BF16_TFLOPS}
+
+
+def bench_qknorm(steps, warmup, dev):
+    import torch
+    from algebraic_amd.kernels import qk_rms_norm
+    gen = torch.Generator(device=dev).manual_seed(3)
+    shape = (8, 2048, 16, 64)
+    xs = [torch.randn(shape, device=dev, generator=gen).bfloat16().requires_grad_(True)
+          for _ in range(2)]
+    gains = [(1 + 0.01 * torch.randn(64, device=dev, generator=gen)).requires_grad_(True)
+             for _ in range(2)]
+    dys = [torch.randn(shape, device=dev, generator=gen).bfloat16() for _ in range(2)]
+
+    def step():
+        for x, g, dy in zip(xs, gains, dys):
+            torch.autograd.grad(qk_rms_norm(x, g), (x, g), dy)
+
+    fp, bp = Probe("qknorm_fwd", steps), Probe("qknorm_bwd", steps)
+    time_steps(step, steps, warmup, fp)
+    time_steps(step, steps, 1, bp)
+    elems = xs[0].numel()
+    # the probe brackets one call; the second tensor's call re-arms nothing, so
+    # each pair holds the last (k) call of its step
+    fwd_bytes, bwd_bytes = elems * 4, elems * 6
+    f_ms, b_ms = fp.mean_ms(), bp.mean_ms()
+    return {"workload": "q,k each [8,2048,16,64] bf16, D=64 rows",
+            "fwd_us": f_ms * 1e3, "fwd_gbs": fwd_bytes / f_ms / 1e6,
+            "bwd_us": b_ms * 1e3, "bwd_gbs": bwd_bytes / b_ms / 1e6,
+            "fwd_frac": fwd_bytes / f_ms / 1e6 / PEAK_HBM_GBS,
+            "bwd_frac": bwd_bytes / b_ms / 1e6 / PEAK_HBM_GBS}
+
+
+def traffic_bytes():
+    """HBM bytes per attention-backward launch measured by rocprofv3 --pmc
+    (FETCH_SIZE + WRITE_SIZE, scaled by a 256 MiB copy), when that summary
+    has been recorded in profiles/attn_bwd_traffic.json; else None."""
+    path = os.path.join(ROOT, "profiles", "attn_bwd_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def cpu_baseline(B, H, T, D, heads=None):
+    # The whole configs[1] workload, twice over (about 10 s on 16 host cores).
+    heads = heads or 2 * B * H
+    from oracle.cpu_baseline import time_attention_fwd_bwd
+    secs, threads = time_attention_fwd_bwd(T=T, D=D, heads=heads)
+    per_head = 3.5 * 4.0 * T * T * D / 2.0
+    return {"value": heads * per_head / secs / 1e12, "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{heads} (b,h)-head fwd+bwd passes ({heads / (B * H):g}x the configs[1] workload of {B * H} heads), dense "
+                      f"algebraic.asinh_attention fwd + autograd bwd in torch-CPU float32, "
+                      f"{secs:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-secondary", action="store_true", help="skip the head/QK-norm lines")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run one plain 256 MiB device copy (scale reference for the "
+                         "FETCH_SIZE/WRITE_SIZE counters of a rocprofv3 --pmc run)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: every box in this build has one MI355X and the hot "
+              "path is sharded by (b, h) heads with no exchange; run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    from algebraic_amd import _lib
+    _lib.load()
+    dev = "cuda:0"
+    B, H, T, D = 8, 12, 2048, 64
+    if args.calibrate_copy:
+        src = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    torch.cuda.synchronize()
+    a = bench_attention(B, H, T, D, args.steps, args.warmup, dev)
+    bwd_achieved = a["bwd_flops"] / (a["bwd_kernel_ms"] * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": round(a["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(a["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "asinh-power causal flash attention fwd+bwd (configs[1])",
+                   "batch": B, "heads": H, "seq_len": T, "head_dim": D, "n": 16, "c": 8.0,
+                   "range_guard": True, "sink": None, "qk_norm_inputs": True},
+        "roofline": {"bound": "mfma", "kernel": "attention backward (bwd_mfma_kernel)",
+                     "achieved": round(bwd_achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(bwd_achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic_bytes(),
+                     "flops_per_launch": a["bwd_flops"],
+                     "avg_launch_ms": round(a["bwd_kernel_ms"], 4)},
+        "step_frac_of_peak": round(a["tflops"] / PEAK_BF16_TFLOPS, 4),
+        "kernels": {
+            "attn_fwd": {"avg_launch_ms": round(a["fwd_kernel_ms"], 4),
+                         "tflops": round(a["fwd_flops"] / a["fwd_kernel_ms"] / 1e9, 2)},
+            "attn_bwd": {"avg_launch_ms": round(a["bwd_kernel_ms"], 4),
+                         "tflops": round(bwd_achieved, 2)},
+        },
+    }
+    if not args.no_secondary:
+        a16 = bench_attention(8, 16, T, D, max(5, args.steps // 2), 2, dev)
+        line["secondary"] = {
+            "attn_h16": {"workload": "configs[3] attention B=8,H=16,T=2048,D=64",
+                         "ms_per_step": round(a16["ms_per_step"], 4),
+                         "tflops": round(a16["tflops"], 2),
+                         "frac": round(a16["tflops"] / PEAK_BF16_TFLOPS, 4)},
+            "fused_head": {k: (round(v, 4) if isinstance(v, float) else v)
+                           for k, v in bench_head(5, 2, dev).items()},
+            "qknorm": {k: (round(v, 4) if isinstance(v, float) else v)
+                       for k, v in bench_qknorm(20, 3, dev).items()},
+        }
+    if not args.no_cpu:
+        line["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                for k, v in cpu_baseline(B, H, T, D).items()}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

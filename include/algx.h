@@ -50,6 +50,23 @@ int32_t algx_version(void);
  * major), bt: B^T as 32x16 bf16 (row major), d: 32x32 float32 = a @ b. */
 int32_t algx_selftest_mfma32(const void* a, const void* bt, float* d, void* stream);
 
+/* Diagnostic without a reference counterpart, for benchmarks: while set, the
+ * named kernel records the caller's HIP events `start` before and `stop` after
+ * its launch, on the stream it is launched on (which = ALGX_PROBE_NONE clears).
+ * The setting is process-wide (backward passes often run on another thread). */
+enum {
+  ALGX_PROBE_NONE = 0,
+  ALGX_PROBE_ATTN_FWD = 1,   /* main attention forward kernel                  */
+  ALGX_PROBE_ATTN_BWD = 2,   /* main attention backward kernel                 */
+  ALGX_PROBE_HEAD_FWD = 3,   /* fused-head forward statistics kernel           */
+  ALGX_PROBE_HEAD_DZ = 4,    /* fused-head backward logit-gradient kernel      */
+  ALGX_PROBE_HEAD_DH = 5,    /* fused-head dh GEMM                             */
+  ALGX_PROBE_HEAD_DE = 6,    /* fused-head dE GEMM                             */
+  ALGX_PROBE_QKNORM_FWD = 7,
+  ALGX_PROBE_QKNORM_BWD = 8
+};
+int32_t algx_set_probe(int32_t which, void* start_event, void* stop_event);
+
 /* ---------------------------------------------------------------- QK norm
  * Replaces qk_rms_norm (src/algebraic/kernels/qk_norm.py:62-76) with its
  * custom VJP (:29-59) and the rms_norm math (src/algebraic/algebraic.py:76-83):
@@ -69,33 +86,33 @@ int32_t algx_qknorm_bwd(const void* x, const float* gain, const void* dy, void* 
  * head_resident.forward head_resident.py:138-155) and the custom VJP
  * (_flash_bwd :718-726, _backward :630-687, head_resident.backward :158-176).
  *
- * q, k, v, o, dout, dq, dk, dv: (B, H, T, D) in `dtype`. The query is passed
- * UNSCALED; kernels form q_s = cast(q * q_scale) on load exactly as
- * flash.py:833 does. sink: (H,) float32 in kernel units (sink_logit / c), or
- * NULL. stat: (B, H, T) float32.
+ * q, q_s, k, v, o, dout, dq, dk, dv: (B, H, T, D) in `dtype`. sink: (H,)
+ * float32 in kernel units (sink_logit / c), or NULL. stat: (B, H, T) float32.
  *
- * Guarded dispatch (flash.py:834-856): algx_attn_guard reduces max|q_s|^2,
- * max|k|^2, max|v| and |sink| into `guard` (algx_attn_guard_words() int32
- * words) and sets guard[0] = 1 when in range. Passing that buffer to the
- * forward/backward selects `low` when guard[0] == 1 and `high` otherwise, on
- * the device, without a host round trip. Passing guard = NULL runs `low`. */
+ * algx_attn_prepare forms the pre-scaled query q_s = cast(q * q_scale)
+ * (flash.py:833) that the forward and backward consume. Given a guard buffer
+ * (algx_attn_guard_words() int32 words) it also reduces max|q_s|^2, max|k|^2,
+ * max|v| and |sink| (flash.py:841-849) in the same pass and sets guard[0] = 1
+ * when in range. Passing that buffer to the forward/backward selects `low`
+ * when guard[0] == 1 and `high` otherwise, on the device, without a host
+ * round trip (flash.py:853-856). guard = NULL runs `low`. */
 int32_t algx_attn_guard_words(void);
-int32_t algx_attn_guard(const void* q, const void* k, const void* v, const float* sink,
-                        int32_t* guard, int32_t B, int32_t H, int32_t T, int32_t D,
-                        int32_t dtype, float q_scale, float bound, float vmax, void* stream);
+int32_t algx_attn_prepare(const void* q, const void* k, const void* v, const float* sink,
+                          void* q_s, int32_t* guard, int32_t B, int32_t H, int32_t T, int32_t D,
+                          int32_t dtype, float q_scale, float bound, float vmax, void* stream);
 
 /* o_precise: float32 (B,H,T,D), written only by a variant with
  * precise_output (may be NULL when no such variant can run). */
-int32_t algx_attn_fwd(const void* q, const void* k, const void* v, const float* sink,
+int32_t algx_attn_fwd(const void* q_s, const void* k, const void* v, const float* sink,
                       void* o, float* o_precise, float* stat, int32_t B, int32_t H, int32_t T,
-                      int32_t D, int32_t dtype, float q_scale, const algx_attn_variant* low,
+                      int32_t D, int32_t dtype, const algx_attn_variant* low,
                       const algx_attn_variant* high, const int32_t* guard, void* stream);
 
 int64_t algx_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t T, int32_t D);
 /* dq is w.r.t. the unscaled q: dq = cast(cast(dq_s) * q_scale) as autodiff of
  * flash.py:833 gives; dsink (H,) float32 is w.r.t. the kernel-unit sink
  * (flash.py:721-723) and may be NULL when sink is NULL. */
-int32_t algx_attn_bwd(const void* q, const void* k, const void* v, const float* sink,
+int32_t algx_attn_bwd(const void* q_s, const void* k, const void* v, const float* sink,
                       const void* o, const float* o_precise, const float* stat, const void* dout,
                       void* dq, void* dk, void* dv, float* dsink, void* workspace, int32_t B,
                       int32_t H, int32_t T, int32_t D, int32_t dtype, float q_scale,

@@ -52,7 +52,7 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     rc = lib.algx_qknorm_fwd(None, None, None, 16, 32, 0, 1e-5, None)
     assert rc != 0 and b"D must be 64" in lib.algx_last_error()
     v = _lib.AttnVariant(kind=1, n=12)
-    rc = lib.algx_attn_fwd(None, None, None, None, None, None, None, 1, 1, 128, 64, 0, 1.0,
+    rc = lib.algx_attn_fwd(None, None, None, None, None, None, None, 1, 1, 128, 64, 0,
                            v, None, None, None)
     assert rc != 0 and b"power of two" in lib.algx_last_error()
     rc = lib.algx_head_fwd(None, None, None, None, None, None, 4, 12, 100, 0, 16, 1.0, 0.0, 0, None)
