@@ -1,20 +1,26 @@
 // gfx950 MFMA attention backward (flash.py:333-361 tile VJP, :630-638;
 // head_resident.py:95-132).
 //
-// One workgroup owns 128 keys of one (b, h) (32 per wave; the wave's K and V
-// rows stay in registers as MFMA B operands) and walks 64-query tiles from
-// the diagonal to T. Each tile is handled as two 32-query halves: S and dP
-// are formed with queries on the M axis, so each lane holds one key column
-// and 16 queries; p and ds are formed in registers and feed
-// dV^T += dO^T P and dK^T += Q_s^T dS directly (dO^T and Q_s^T are staged
-// transposed in LDS with the k-slot order the accumulator layout implies).
-// The next half's S/dP MFMAs are issued before the current half's dV/dK
-// MFMAs so the MFMA pipe runs under the VALU weight/gradient math.
+// One workgroup of 8 waves owns 256 keys of one (b, h) (32 per wave; the
+// wave's K and V rows stay in registers as MFMA B operands) and walks 64-query
+// tiles from the diagonal to T. Per 32-query half of a tile, S and dP are
+// formed with queries on the M axis, so each lane holds one key and 16
+// queries. dP already carries -di: one extra MFMA k-block multiplies
+// [-di_hi, -di_lo] (di split into two bf16 parts) by a ones column of V.
+// p and ds are formed in registers and feed dV^T += dO^T P and
+// dK^T += Q_s^T dS directly; dO^T and Q_s^T come from the row-major LDS tiles
+// through transposing LDS reads (ds_read_b64_tr_b16) in the k-slot order the
+// accumulator layout implies, so no transposed copy is ever stored.
 //
-// dS goes through LDS once, so that the four waves together form the
-// workgroup's dQ tile (64 queries x 64 d over 128 keys), which is added into
-// a float32 dQ accumulator with no-return atomics; workgroups of one head sit
-// on one XCD, so those atomics resolve in that XCD's L2.
+// dS^T goes to LDS once ([key][query], 8-byte stores), and each wave then
+// forms a 16-query x 32-d block of the tile's dQ over all 256 keys with
+// v_mfma_f32_16x16x32_bf16 (dS and K both read through transposing reads) and
+// adds it to a float32 accumulator with no-return atomics: one add per
+// element per 256 keys.
+//
+// Pipelining: Q_s/dO/stat/di tiles and dS^T are double-buffered in LDS, so a
+// tile needs one barrier. The dQ of tile t-1 is formed while tile t's
+// weights are computed, and tile t+2 is fetched from HBM while tile t runs.
 #include <type_traits>
 
 #include "attn_mfma.h"
@@ -23,32 +29,57 @@ namespace algx {
 namespace mfma {
 namespace {
 
-// p and ds of one score (flash.py:339-361); ds already multiplied by r.
+constexpr int BKN = 256;   // keys per workgroup
+constexpr int BQ = 64;     // queries per tile
+constexpr int NWAVE = 8;
+constexpr int NTHR = 64 * NWAVE;
+constexpr int RSTR = 72;   // LDS row stride (bf16) of the Q_s, dO, K and dS^T tiles
+
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Transposing LDS read: lane 4j+m of each 16-lane group addresses 4
+// consecutive bf16 of row j; lane i of the group receives element i%4 of the
+// rows addressed by lanes i/4, i/4+4, i/4+8, i/4+12.
+__device__ __forceinline__ bf16x4 read_tr(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+}
+
+__device__ __forceinline__ bf16x8 join(bf16x4 a, bf16x4 b) {
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// p and ds of one score (flash.py:339-361); dpp = dP - di, ds already
+// multiplied by r. For the unshifted kernels `st` is the row factor with
+// p = rho^n * st: the statistic itself when it is 1/Z (inv_stat), its n-th
+// power otherwise ((rho * Z^(-1/n))^n = rho^n / Z, rho being clamped so rho^n
+// is finite).
 template <int MODE, bool FAST, bool BOUNDED, int L2N>
-__device__ __forceinline__ void tile_grad(float s, float dp, float st, float dd, float clamp,
-                                          int log2n, bool inv_stat, float& p, float& ds) {
+__device__ __forceinline__ void tile_grad(float s, float dpp, float st, float clamp, int log2n,
+                                          float& p, float& ds) {
   if (MODE == MODE_SOFTMAX) {
     p = __builtin_amdgcn_exp2f((s - st) * kLog2e);
-    ds = p * (dp - dd);
+    ds = p * dpp;
     return;
   }
   const float x = (MODE == MODE_NOSHIFT && !BOUNDED) ? __builtin_fminf(s, clamp) : s;
   float r;
   const float rh = FAST ? rho_fast(x, r) : rho_exact(x, r);
-  p = (MODE == MODE_NOSHIFT && inv_stat) ? powN<L2N>(rh, log2n) * st : powN<L2N>(rh * st, log2n);
-  ds = p * (dp - dd) * r;
+  p = MODE == MODE_NOSHIFT ? powN<L2N>(rh, log2n) * st : powN<L2N>(rh * st, log2n);
+  ds = (p * r) * dpp;
   if (MODE == MODE_NOSHIFT && !BOUNDED && !(s < clamp)) ds = 0.0f;
 }
 
 struct BwdLds {
-  bf16* Qs;
-  bf16* Gs;
-  bf16* Qt;
-  bf16* Gt;
-  float* St;
-  float* Dt;
-  bf16* dSs;
-  bf16* Kt;
+  bf16 q[2][BQ * RSTR];     // Q_s tile, row-major [query][d]
+  bf16 g[2][BQ * RSTR];     // dO tile
+  float st[2][BQ];          // statistic (or its row factor)
+  float dd[2][BQ];          // di
+  bf16 dst[2][BKN * RSTR];  // dS^T [key][query]
+  bf16 k[BKN * RSTR];       // K rows of the workgroup [key][d]
 };
 
 template <int MODE, bool FAST, bool BOUNDED, int L2N>
@@ -56,39 +87,46 @@ __device__ __forceinline__ void bwd_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ stat, const float* __restrict__ di, const bf16* __restrict__ dout,
     float* __restrict__ dq_acc, bf16* __restrict__ dk, bf16* __restrict__ dv, int T_,
-    const KVariant& var, const BwdLds& L) {
-  const int nkb = T_ / BBN;
+    const KVariant& var, BwdLds& L) {
+  const int nkb = (T_ + BKN - 1) / BKN;
   const int nheads = gridDim.x / nkb;
   int bh, kb;
   map_block(blockIdx.x, nheads, nkb, false, bh, kb);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
+  const int G = lane >> 4, i16 = lane & 15, j4 = i16 >> 2, m4 = i16 & 3;
   const int64_t base = (int64_t)bh * T_ * HD;
   const int64_t rbase = (int64_t)bh * T_;
-  const int key0 = kb * BBN, kw = key0 + 32 * w, kcol = kw + c32;
+  const int key0 = kb * BKN, kw = key0 + 32 * w, kcol = kw + c32;
+  const bool wave_keys = kw < T_;  // T % 64 == 0: a wave's 32 keys are all valid or none
   const int log2n = var.log2n;
-  const bool inv_stat = var.inv_stat;
+  const bool stat_pow = MODE == MODE_NOSHIFT && !var.inv_stat;
   const float clamp = var.clamp;
 
   // B operands: lane holds K[kcol][16ks + 8g ..] and V[kcol][16ks + 8g ..].
   bf16x8 kreg[4], vreg[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    kreg[ks] = *reinterpret_cast<const bf16x8*>(k + base + (int64_t)kcol * HD + 16 * ks + 8 * g);
-    vreg[ks] = *reinterpret_cast<const bf16x8*>(v + base + (int64_t)kcol * HD + 16 * ks + 8 * g);
-  }
-  // K^T of the workgroup's 128 keys (natural key order) for the dQ product.
-  {
-    const int kg = tid >> 3, dc = tid & 7;
-    bf16x8 rows[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      rows[i] = *reinterpret_cast<const bf16x8*>(k + base + (int64_t)(key0 + 4 * kg + i) * HD +
-                                                 8 * dc);
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      bf16x4 col = {rows[0][d], rows[1][d], rows[2][d], rows[3][d]};
-      *reinterpret_cast<bf16x4*>(&L.Kt[(8 * dc + d) * KTSTR + 4 * kg]) = col;
+    if (wave_keys) {
+      kreg[ks] = *reinterpret_cast<const bf16x8*>(k + base + (int64_t)kcol * HD + 16 * ks + 8 * g);
+      vreg[ks] = *reinterpret_cast<const bf16x8*>(v + base + (int64_t)kcol * HD + 16 * ks + 8 * g);
+    } else {
+      kreg[ks] = bf16x8{};
+      vreg[ks] = bf16x8{};
     }
+  }
+  // Ones in the k rows 64, 65 of the extended V^T (dP's -di block).
+  const bf16 one = (bf16)1.0f, zero = (bf16)0.0f;
+  const bf16x8 ones = g == 0 ? bf16x8{one, one, zero, zero, zero, zero, zero, zero} : bf16x8{};
+  // K rows of the workgroup, row-major, for the dQ product; dS^T buffer 1
+  // starts zeroed because the first tile's dQ step reads it.
+#pragma unroll
+  for (int i = 0; i < BKN * HD / 8 / NTHR; ++i) {
+    const int c = tid + NTHR * i, row = c >> 3, col = 8 * (c & 7);
+    const bf16x8 val =
+        key0 + row < T_ ? *reinterpret_cast<const bf16x8*>(k + base + (int64_t)(key0 + row) * HD + col)
+                        : bf16x8{};
+    *reinterpret_cast<bf16x8*>(&L.k[row * RSTR + col]) = val;
+    *reinterpret_cast<bf16x8*>(&L.dst[1][row * RSTR + col]) = bf16x8{};
   }
 
   f32x16 dka[2], dva[2];
@@ -98,68 +136,61 @@ __device__ __forceinline__ void bwd_body(
     zero16(dva[dt]);
   }
 
-  // Loaders: threads 0..127 move Q_s rows, 128..255 move dO rows, 4
-  // consecutive queries x 8 d each; threads 0..63 also move stat and di.
-  const bool qloader = tid < 128;
-  const int u = tid & 127, qg = u >> 3, dc = u & 7;
-  bf16x8 pre[4];
+  // Tile loader: thread t moves Q_s and dO row t/8, d 8(t%8) .. +7; threads
+  // 0..63 also move stat and di of query t.
+  const int lrow = tid >> 3, lcol = 8 * (tid & 7);
+  bf16x8 preq, preg;
   float pst = 0.0f, pdi = 0.0f;
+  const int qt0 = key0 / BQ, nqt = T_ / BQ;
   auto gload = [&](int qt) {
-    const int64_t row0 = (int64_t)(qt * BBM + 4 * qg);
-    const bf16* src = (qloader ? q : dout) + base + row0 * HD + 8 * dc;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pre[i] = *reinterpret_cast<const bf16x8*>(src + i * HD);
-    if (tid < BBM) {
-      pst = stat[rbase + qt * BBM + tid];
-      pdi = di[rbase + qt * BBM + tid];
+    const int64_t off = base + (int64_t)(qt * BQ + lrow) * HD + lcol;
+    preq = *reinterpret_cast<const bf16x8*>(q + off);
+    preg = *reinterpret_cast<const bf16x8*>(dout + off);
+    if (tid < BQ) {
+      pst = stat[rbase + qt * BQ + tid];
+      pdi = di[rbase + qt * BQ + tid];
     }
   };
-  auto lstore = [&]() {
-    bf16* rowbuf = qloader ? L.Qs : L.Gs;
-    bf16* tbuf = qloader ? L.Qt : L.Gt;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<bf16x8*>(&rowbuf[(4 * qg + i) * QSTR + 8 * dc]) = pre[i];
-    const int pos = 16 * (qg >> 2) + slot_pos(4 * (qg & 3));
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      bf16x4 col = {pre[0][d], pre[1][d], pre[2][d], pre[3][d]};
-      *reinterpret_cast<bf16x4*>(&tbuf[(8 * dc + d) * QTSTR + pos]) = col;
-    }
-    if (tid < BBM) {
-      L.St[tid] = pst;
-      L.Dt[tid] = pdi;
+  auto lstore = [&](int buf) {
+    *reinterpret_cast<bf16x8*>(&L.q[buf][lrow * RSTR + lcol]) = preq;
+    *reinterpret_cast<bf16x8*>(&L.g[buf][lrow * RSTR + lcol]) = preg;
+    if (tid < BQ) {
+      L.st[buf][tid] = stat_pow ? powN<L2N>(pst, log2n) : pst;
+      L.dd[buf][tid] = pdi;
     }
   };
 
-  // S and dP of query half mq: acc[r] <-> query 32mq + 8(r/4) + 4g + r%4, key kcol.
-  auto half_scores = [&](int mq, f32x16& s, f32x16& dp) {
+  // S and dP - di of query half mq: acc[r] <-> query 32mq + 8(r/4) + 4g + r%4, key kcol.
+  auto half_scores = [&](int buf, int mq, f32x16& s, f32x16& dp) {
     zero16(s);
     zero16(dp);
+    const bf16* qrow = &L.q[buf][(32 * mq + c32) * RSTR + 8 * g];
+    const bf16* grow = &L.g[buf][(32 * mq + c32) * RSTR + 8 * g];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 aq = *reinterpret_cast<const bf16x8*>(&L.Qs[(32 * mq + c32) * QSTR + 16 * ks + 8 * g]);
-      const bf16x8 ag = *reinterpret_cast<const bf16x8*>(&L.Gs[(32 * mq + c32) * QSTR + 16 * ks + 8 * g]);
-      s = mfma32(aq, kreg[ks], s);
-      dp = mfma32(ag, vreg[ks], dp);
+      s = mfma32(*reinterpret_cast<const bf16x8*>(qrow + 16 * ks), kreg[ks], s);
+      dp = mfma32(*reinterpret_cast<const bf16x8*>(grow + 16 * ks), vreg[ks], dp);
     }
+    const float dd = L.dd[buf][32 * mq + c32];
+    const bf16 hi = (bf16)dd;
+    const bf16 lo = (bf16)(dd - (float)hi);
+    const bf16x8 aext = g == 0 ? bf16x8{-hi, -lo, zero, zero, zero, zero, zero, zero} : bf16x8{};
+    dp = mfma32(aext, ones, dp);
   };
   // p, ds of half mq -> bf16 k-slot packs (two 16-query chunks each). Only
   // tiles that cross the diagonal (diag_tag = true_type) evaluate the mask.
-  auto half_grads = [&](auto diag_tag, int q0, int mq, const f32x16& s, const f32x16& dp,
-                        bf16x8 (&pb)[2], bf16x8 (&db)[2]) {
+  auto half_grads = [&](auto diag_tag, int buf, int q0, int mq, const f32x16& s,
+                        const f32x16& dp, bf16x8 (&pb)[2], bf16x8 (&db)[2]) {
     constexpr bool DIAG = decltype(diag_tag)::value;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int qo = 32 * mq + 8 * j + 4 * g;
-      const f32x4 st4 = *reinterpret_cast<const f32x4*>(&L.St[qo]);
-      const f32x4 di4 = *reinterpret_cast<const f32x4*>(&L.Dt[qo]);
+      const f32x4 st4 = *reinterpret_cast<const f32x4*>(&L.st[buf][qo]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * j + i;
         float p, ds;
-        tile_grad<MODE, FAST, BOUNDED, L2N>(s[r], dp[r], st4[i], di4[i], clamp, log2n, inv_stat,
-                                            p, ds);
+        tile_grad<MODE, FAST, BOUNDED, L2N>(s[r], dp[r], st4[i], clamp, log2n, p, ds);
         if (DIAG && q0 + qo + i < kcol) {
           p = 0.0f;
           ds = 0.0f;
@@ -169,79 +200,129 @@ __device__ __forceinline__ void bwd_body(
       }
     }
   };
-  // dV^T += dO^T P and dK^T += Q_s^T dS over the half's two 16-query chunks;
-  // dS of the half -> LDS as [query][key].
-  auto half_update = [&](int mq, const bf16x8 (&pb)[2], const bf16x8 (&db)[2]) {
+  // dV^T += dO^T P and dK^T += Q_s^T dS over the half's two 16-query chunks
+  // (A operands through transposing reads); dS^T of the half -> LDS.
+  auto half_update = [&](int buf, int mq, const bf16x8 (&pb)[2], const bf16x8 (&db)[2]) {
 #pragma unroll
     for (int kcl = 0; kcl < 2; ++kcl) {
-      const int kc = 2 * mq + kcl;
+      const int qbase = 16 * (2 * mq + kcl) + 4 * (G >> 1) + j4;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
-        const bf16x8 ag = *reinterpret_cast<const bf16x8*>(&L.Gt[(32 * dt + c32) * QTSTR + 16 * kc + 8 * g]);
-        const bf16x8 aq = *reinterpret_cast<const bf16x8*>(&L.Qt[(32 * dt + c32) * QTSTR + 16 * kc + 8 * g]);
+        const int col = 32 * dt + 16 * (G & 1) + 4 * m4;
+        const bf16x8 ag = join(read_tr(&L.g[buf][qbase * RSTR + col]),
+                               read_tr(&L.g[buf][(qbase + 8) * RSTR + col]));
+        const bf16x8 aq = join(read_tr(&L.q[buf][qbase * RSTR + col]),
+                               read_tr(&L.q[buf][(qbase + 8) * RSTR + col]));
         dva[dt] = mfma32(ag, pb[kcl], dva[dt]);
         dka[dt] = mfma32(aq, db[kcl], dka[dt]);
       }
     }
+    bf16* drow = &L.dst[buf][(32 * w + c32) * RSTR + 32 * mq + 4 * g];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int qo = 32 * mq + 8 * (r >> 2) + 4 * g + (r & 3);
-      L.dSs[qo * DSSTR + 32 * w + c32] = db[r >> 3][r & 7];
+    for (int kcl = 0; kcl < 2; ++kcl) {
+      *reinterpret_cast<bf16x4*>(drow + 16 * kcl) =
+          bf16x4{db[kcl][0], db[kcl][1], db[kcl][2], db[kcl][3]};
+      *reinterpret_cast<bf16x4*>(drow + 16 * kcl + 8) =
+          bf16x4{db[kcl][4], db[kcl][5], db[kcl][6], db[kcl][7]};
+    }
+  };
+  auto zero_dst = [&](int buf) {
+    bf16* drow = &L.dst[buf][(32 * w + c32) * RSTR + 4 * g];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<bf16x4*>(drow + 8 * j) = bf16x4{};
+  };
+  // dQ of tile qt from dS^T[buf]: wave w forms queries 16(w%4).., d 32(w/4)..
+  // over the 256 keys (16x16x32 MFMAs), then adds it to the accumulator.
+  auto dq_tile = [&](int qt, int buf) {
+    const int qr = 16 * (w & 3), dc = 32 * (w >> 2);
+    f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+    // Two k-steps per loop trip: a full unroll lets the scheduler hoist all
+    // 48 operand reads and spill.
+#pragma unroll 2
+    for (int kk = 0; kk < BKN / 32; ++kk) {
+      const int krow = 32 * kk + 8 * G + j4;
+      const bf16x8 a = join(read_tr(&L.dst[buf][krow * RSTR + qr + 4 * m4]),
+                            read_tr(&L.dst[buf][(krow + 4) * RSTR + qr + 4 * m4]));
+      const bf16x8 b0 = join(read_tr(&L.k[krow * RSTR + dc + 4 * m4]),
+                             read_tr(&L.k[(krow + 4) * RSTR + dc + 4 * m4]));
+      const bf16x8 b1 = join(read_tr(&L.k[krow * RSTR + dc + 16 + 4 * m4]),
+                             read_tr(&L.k[(krow + 4) * RSTR + dc + 16 + 4 * m4]));
+      acc0 = mfma16(a, b0, acc0);
+      acc1 = mfma16(a, b1, acc1);
+    }
+    // acc[i]: dQ[qt*64 + qr + 4G + i][dc + 16nb + i16]
+    float* dst = dq_acc + base + (int64_t)(qt * BQ + qr + 4 * G) * HD + dc + i16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      atomicAdd(dst + (int64_t)i * HD, acc0[i]);
+      atomicAdd(dst + (int64_t)i * HD + 16, acc1[i]);
     }
   };
 
-  const int qt0 = key0 / BBM, nqt = T_ / BBM;
+  // Prologue: tile qt0 into buffer 0, tile qt0+1 in registers; the explicit
+  // drains keep the loop's memory-counter waits from covering prologue loads
+  // (the counter retires in order, so such a wait would also wait for the
+  // dQ atomics issued later in each iteration).
   gload(qt0);
-  for (int qt = qt0; qt < nqt; ++qt) {
-    __syncthreads();  // previous tile's LDS reads are done
-    lstore();
-    __syncthreads();
-    if (qt + 1 < nqt) gload(qt + 1);
-    const int q0 = qt * BBM;
-    if (q0 + BBM - 1 >= kw) {
-      const bool diag = q0 < kw + 31;
-      f32x16 s0, dp0, s1, dp1;
-      bf16x8 pb0[2], db0[2], pb1[2], db1[2];
-      half_scores(0, s0, dp0);
-      if (diag)
-        half_grads(std::true_type{}, q0, 0, s0, dp0, pb0, db0);
-      else
-        half_grads(std::false_type{}, q0, 0, s0, dp0, pb0, db0);
-      half_scores(1, s1, dp1);
-      half_update(0, pb0, db0);
-      if (diag)
-        half_grads(std::true_type{}, q0, 1, s1, dp1, pb1, db1);
-      else
-        half_grads(std::false_type{}, q0, 1, s1, dp1, pb1, db1);
-      half_update(1, pb1, db1);
-    } else {
-#pragma unroll
-      for (int mq = 0; mq < 2; ++mq)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qo = 32 * mq + 8 * (r >> 2) + 4 * g + (r & 3);
-          L.dSs[qo * DSSTR + 32 * w + c32] = (bf16)0.0f;
-        }
-    }
-    __syncthreads();
-    // dQ tile: wave w forms queries 32*(w/2).., d 32*(w%2).. over 128 keys.
-    {
-      const int mq = w >> 1, dt = w & 1;
-      f32x16 acc;
-      zero16(acc);
-#pragma unroll
-      for (int kk = 0; kk < BBN / 16; ++kk) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&L.dSs[(32 * mq + c32) * DSSTR + 16 * kk + 8 * g]);
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(&L.Kt[(32 * dt + c32) * KTSTR + 16 * kk + 8 * g]);
-        acc = mfma32(a, b, acc);
-      }
-      // acc[r]: dQ[q0 + 32mq + 8(r/4) + 4g + r%4][32dt + c32]
-      float* dst = dq_acc + base + (int64_t)(q0 + 32 * mq + 4 * g) * HD + 32 * dt + c32;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) atomicAdd(dst + (int64_t)(8 * (r >> 2) + (r & 3)) * HD, acc[r]);
-    }
-  }
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  lstore(0);
+  gload(qt0 + 1 < nqt ? qt0 + 1 : qt0);
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  __syncthreads();
 
+  // Every iteration has the same memory-operation sequence (dQ atomics of the
+  // previous tile, LDS store of the next tile, fetch of the one after), so
+  // each wait covers exactly the fetch issued one iteration earlier. Tile
+  // indices past the end are clamped: that extra work lands in buffers no
+  // later step reads, or adds zeros.
+  const int qdiag = qt0 + BKN / BQ < nqt ? qt0 + BKN / BQ : nqt;
+  int qt = qt0;
+  for (; qt < qdiag; ++qt) {
+    const int buf = (qt - qt0) & 1;
+    const int q0 = qt * BQ;
+    if (wave_keys && q0 + BQ - 1 >= kw) {
+      const bool diag = q0 < kw + 31;
+#pragma unroll
+      for (int mq = 0; mq < 2; ++mq) {
+        f32x16 s, dp;
+        bf16x8 pb[2], db[2];
+        half_scores(buf, mq, s, dp);
+        if (diag)
+          half_grads(std::true_type{}, buf, q0, mq, s, dp, pb, db);
+        else
+          half_grads(std::false_type{}, buf, q0, mq, s, dp, pb, db);
+        half_update(buf, mq, pb, db);
+      }
+    } else {
+      zero_dst(buf);
+    }
+    dq_tile(qt > qt0 ? qt - 1 : qt0, buf ^ 1);
+    lstore(buf ^ 1);
+    gload(qt + 2 < nqt ? qt + 2 : nqt - 1);
+    __syncthreads();
+  }
+  // Tiles below the diagonal: no masks and no per-wave branches, so the
+  // MFMAs of one half interleave with the weight math of the other in a
+  // single basic block.
+  for (; qt < nqt; ++qt) {
+    const int buf = (qt - qt0) & 1;
+    const int q0 = qt * BQ;
+    f32x16 s0, dp0, s1, dp1;
+    bf16x8 pb0[2], db0[2], pb1[2], db1[2];
+    half_scores(buf, 0, s0, dp0);
+    half_grads(std::false_type{}, buf, q0, 0, s0, dp0, pb0, db0);
+    half_scores(buf, 1, s1, dp1);
+    half_update(buf, 0, pb0, db0);
+    half_grads(std::false_type{}, buf, q0, 1, s1, dp1, pb1, db1);
+    half_update(buf, 1, pb1, db1);
+    dq_tile(qt - 1, buf ^ 1);
+    lstore(buf ^ 1);
+    gload(qt + 2 < nqt ? qt + 2 : nqt - 1);
+    __syncthreads();
+  }
+  dq_tile(nqt - 1, (nqt - 1 - qt0) & 1);
+
+  if (!wave_keys) return;
   // dka[dt][r]: dK[kcol][32dt + 8(r/4) + 4g + r%4] (before the slope n).
   const int64_t krow = base + (int64_t)kcol * HD;
   const float slope = var.slope;
@@ -260,20 +341,12 @@ __device__ __forceinline__ void bwd_body(
 }
 
 template <int LO, int HI>
-__global__ __launch_bounds__(256, 2) void bwd_mfma_kernel(
+__global__ __launch_bounds__(NTHR, 1) void bwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ stat, const float* __restrict__ di, const bf16* __restrict__ dout,
     float* __restrict__ dq_acc, bf16* __restrict__ dk, bf16* __restrict__ dv, int T_,
     KVariant lo, KVariant hi, const int32_t* __restrict__ guard) {
-  __shared__ __attribute__((aligned(16))) bf16 Qs[BBM * QSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Gs[BBM * QSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Qt[HD * QTSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Gt[HD * QTSTR];
-  __shared__ __attribute__((aligned(16))) float St[BBM];
-  __shared__ __attribute__((aligned(16))) float Dt[BBM];
-  __shared__ __attribute__((aligned(16))) bf16 dSs[BBM * DSSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Kt[HD * KTSTR];
-  const BwdLds lds{Qs, Gs, Qt, Gt, St, Dt, dSs, Kt};
+  __shared__ __attribute__((aligned(16))) BwdLds lds;
   if (LO == HI || guard_in_range(guard))
     bwd_body<LO & 3, (LO & 4) != 0, (LO & 8) != 0, (LO >> 4)>(q, k, v, stat, di, dout, dq_acc, dk,
                                                               dv, T_, lo, lds);
@@ -296,12 +369,13 @@ int32_t launch_bwd_mfma(const void* q, const void* k, const void* v, const float
                         int B, int H, int T, const KVariant& lo, const KVariant& hi,
                         const int32_t* guard, hipStream_t s) {
   using namespace mfma;
-  const int grid = B * H * (T / BBN);
+  if (T % BQ != 0 || T < BQ) return fail("attn_bwd: MFMA kernel needs T % 64 == 0");
+  const int grid = B * H * ((T + BKN - 1) / BKN);
   BwdFn fn = pick_bwd(cfg_for(lo), guard != nullptr ? cfg_for(hi) : cfg_for(lo));
   if (fn == nullptr) return fail("attn_bwd: no MFMA kernel for this variant pair");
   ProbeScope probe(ALGX_PROBE_ATTN_BWD, s);
-  fn<<<grid, 256, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)v, stat, di,
-                          (const bf16*)dout, dq_acc, (bf16*)dk, (bf16*)dv, T, lo, hi, guard);
+  fn<<<grid, NTHR, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)v, stat, di,
+                           (const bf16*)dout, dq_acc, (bf16*)dk, (bf16*)dv, T, lo, hi, guard);
   return check_launch("attn_bwd_mfma");
 }
 

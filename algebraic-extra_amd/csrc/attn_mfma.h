@@ -20,6 +20,10 @@ constexpr int KTSTR = 136;  // K^T row stride (128 keys)
 
 enum { MODE_SOFTMAX = 0, MODE_NOSHIFT = 1, MODE_SHIFT = 2 };
 
+// s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt left unconstrained
+// (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4], lgkmcnt[11:8]).
+constexpr int kWaitVm0 = 0x0F70;
+
 // Kernel configuration packed in one int: MODE | FAST << 2 | BOUNDED << 3 | L2N << 4.
 constexpr int cfg_of(int mode, bool fast, bool bounded, int l2n) {
   return mode | (fast ? 4 : 0) | (bounded ? 8 : 0) | (l2n << 4);
