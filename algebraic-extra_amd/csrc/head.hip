@@ -20,7 +20,8 @@ namespace algx {
 namespace {
 
 constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int LSTR = BK + 8;  // LDS row stride (bf16): 144 B
+constexpr int LSTR = BK + 8;  // LDS row stride (bf16) of k-contiguous tiles: 144 B
+constexpr int TSTR = BM + 16;  // LDS row stride (bf16) of [k][mn] tiles: 288 B
 constexpr int kThreads = 256;
 constexpr int kVocabChunkTiles = 16;  // vocabulary tiles per forward workgroup
 
@@ -74,15 +75,34 @@ struct TileLoader {
         *reinterpret_cast<bf16x8*>(lds + (id >> 3) * LSTR + (id & 7) * 8) = r[c];
       }
     } else {
+      // Kept as stored in memory, [k][mn]; the MFMA operand is read through
+      // transposing LDS reads.
       const int kg = tid >> 4, mg = tid & 15;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        bf16x4 col = {r[0][e], r[1][e], r[2][e], r[3][e]};
-        *reinterpret_cast<bf16x4*>(lds + (8 * mg + e) * LSTR + 4 * kg) = col;
-      }
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<bf16x8*>(lds + (4 * kg + i) * TSTR + 8 * mg) = r[i];
     }
   }
 };
+
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+// MFMA operand (rows mn0 + (lane % 32), k-slots k0 + 8(lane / 32) .. +7) of a
+// tile in LDS: one 16-byte read from a [mn][k] tile, or two transposing reads
+// (ds_read_b64_tr_b16) from a [k][mn] tile, in which lane 4j+m of each
+// 16-lane group addresses row j, columns 4m .. 4m+3.
+template <bool KC>
+__device__ __forceinline__ bf16x8 operand(const bf16* tile, int mn0, int k0, int lane) {
+  if (KC) {
+    return *reinterpret_cast<const bf16x8*>(tile + (mn0 + (lane & 31)) * LSTR + k0 + 8 * (lane >> 5));
+  } else {
+    const int G = lane >> 4, j = (lane >> 2) & 3, m = lane & 3;
+    const bf16* p = tile + (k0 + 8 * (G >> 1) + j) * TSTR + mn0 + 16 * (G & 1) + 4 * m;
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * TSTR));
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+}
 
 // acc[i][j][r] = C[m0 + 64wm + 32i + 8(r/4) + 4g + r%4][n0 + 64wn + 32j + c32]
 struct Acc {
@@ -97,17 +117,16 @@ struct Acc {
   }
 };
 
+template <bool AKC, bool BKC>
 __device__ __forceinline__ void mma_stage(const bf16* As, const bf16* Bs, Acc& acc, int wm,
-                                          int wn, int g, int c32) {
+                                          int wn, int lane) {
 #pragma unroll
   for (int ks = 0; ks < BK / 16; ++ks) {
     bf16x8 a[2], b[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      a[i] = *reinterpret_cast<const bf16x8*>(As + (64 * wm + 32 * i + c32) * LSTR + 16 * ks + 8 * g);
+    for (int i = 0; i < 2; ++i) a[i] = operand<AKC>(As, 64 * wm + 32 * i, 16 * ks, lane);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      b[j] = *reinterpret_cast<const bf16x8*>(Bs + (64 * wn + 32 * j + c32) * LSTR + 16 * ks + 8 * g);
+    for (int j = 0; j < 2; ++j) b[j] = operand<BKC>(Bs, 64 * wn + 32 * j, 16 * ks, lane);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -138,7 +157,7 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
       la.load(A, m0, (kk + 1) * BK, tid);
       lb.load(B, n0, (kk + 1) * BK, tid);
     }
-    mma_stage(As + buf * BM * LSTR, Bs + buf * BN * LSTR, acc, wm, wn, g, c32);
+    mma_stage<AKC, BKC>(As + buf * BM * LSTR, Bs + buf * BN * LSTR, acc, wm, wn, lane);
     if (kk + 1 < nk) {
       la.store(As + (buf ^ 1) * BM * LSTR, tid);
       lb.store(Bs + (buf ^ 1) * BN * LSTR, tid);
