@@ -35,21 +35,8 @@ constexpr int NWAVE = 8;
 constexpr int NTHR = 64 * NWAVE;
 constexpr int RSTR = 72;   // LDS row stride (bf16) of the Q_s, dO, K and dS^T tiles
 
-typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// Transposing LDS read: lane 4j+m of each 16-lane group addresses 4
-// consecutive bf16 of row j; lane i of the group receives element i%4 of the
-// rows addressed by lanes i/4, i/4+4, i/4+8, i/4+12.
-__device__ __forceinline__ bf16x4 read_tr(const bf16* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
-}
-
-__device__ __forceinline__ bf16x8 join(bf16x4 a, bf16x4 b) {
-  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
 // p and ds of one score (flash.py:339-361); dpp = dP - di, ds already

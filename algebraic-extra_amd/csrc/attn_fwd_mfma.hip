@@ -7,7 +7,8 @@
 // lane holds 16 keys of ONE query row. The asinh/softmax weight, the causal
 // mask and the row sum run on those registers; the bf16 weights go straight
 // back as the B operand of O^T += V^T P^T, whose A operand is a V^T tile in
-// LDS written with the k-slot order the accumulator layout implies.
+// LDS read through transposing LDS reads in the k-slot order the accumulator
+// layout implies.
 //
 // Software pipeline: the score MFMAs of tile j+1 are issued before the VALU
 // transform of tile j, so the MFMA pipe works while the VALU (the bound of
@@ -28,12 +29,13 @@ __device__ __forceinline__ void fwd_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
     float* __restrict__ stat, int H, int T_, const KVariant& var, bf16 (*Ks)[FBN * KSTR],
-    bf16 (*Vt)[HD * VSTR]) {
+    bf16 (*Vs)[FBN * VSTR]) {
   const int nheads = gridDim.x / (T_ / FBM);
   int bh, qb;
   map_block(blockIdx.x, nheads, T_ / FBM, true, bh, qb);
   const int h = bh % H;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
+  const int G = lane >> 4, j4 = (lane >> 2) & 3, m4 = lane & 3;
   const int64_t base = (int64_t)bh * T_ * HD;
   const int q0 = qb * FBM, qw = q0 + 32 * w, qrow = qw + c32;
   const int log2n = var.log2n;
@@ -55,42 +57,26 @@ __device__ __forceinline__ void fwd_body(
   zero16(oacc[0]);
   zero16(oacc[1]);
 
-  // Loaders: threads 0..127 move K tiles (row-major), 128..255 move V tiles
-  // (4 keys x 8 d each, transposed into V^T on the LDS store).
+  // Loaders: threads 0..127 move K tiles, 128..255 move V tiles, both kept
+  // row-major ([key][d]) in LDS.
   bf16x8 pre[4];
   const bool kloader = tid < 128;
   const int u = tid & 127;
   const int nkb = (q0 + FBM) / FBN;
   auto gload = [&](int kb) {
     const bf16* src = (kloader ? k : v) + base + (int64_t)kb * FBN * HD;
-    if (kloader) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int id = u + 128 * c;
-        pre[c] = *reinterpret_cast<const bf16x8*>(src + (id >> 3) * HD + (id & 7) * 8);
-      }
-    } else {
-      const int kg = u >> 3, dc = u & 7;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        pre[i] = *reinterpret_cast<const bf16x8*>(src + (4 * kg + i) * HD + 8 * dc);
+    for (int c = 0; c < 4; ++c) {
+      const int id = u + 128 * c;
+      pre[c] = *reinterpret_cast<const bf16x8*>(src + (id >> 3) * HD + (id & 7) * 8);
     }
   };
   auto lstore = [&](int buf) {
-    if (kloader) {
+    bf16* dst = kloader ? Ks[buf] : Vs[buf];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int id = u + 128 * c;
-        *reinterpret_cast<bf16x8*>(&Ks[buf][(id >> 3) * KSTR + (id & 7) * 8]) = pre[c];
-      }
-    } else {
-      const int kg = u >> 3, dc = u & 7;
-      const int pos = 16 * (kg >> 2) + slot_pos(4 * (kg & 3));
-#pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        bf16x4 col = {pre[0][d], pre[1][d], pre[2][d], pre[3][d]};
-        *reinterpret_cast<bf16x4*>(&Vt[buf][(8 * dc + d) * VSTR + pos]) = col;
-      }
+    for (int c = 0; c < 4; ++c) {
+      const int id = u + 128 * c;
+      *reinterpret_cast<bf16x8*>(&dst[(id >> 3) * KSTR + (id & 7) * 8]) = pre[c];
     }
   };
   // Tile each loader group fetches in iteration kb (K two ahead, V one ahead).
@@ -196,7 +182,10 @@ __device__ __forceinline__ void fwd_body(
         for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
       m_row = m_new;
     }
-    // O^T += V^T P^T over four 16-key chunks.
+    // O^T += V^T P^T over four 16-key chunks. k-slot s of lane group g holds
+    // key 16kc + 8(s/4) + 4g + s%4 (the accumulator rows the lane owns); the
+    // V^T operand is read from the row-major V tile with two transposing
+    // reads whose row order matches.
     const int buf = kb & 1;
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
@@ -204,11 +193,11 @@ __device__ __forceinline__ void fwd_body(
       bf16x8 pb;
 #pragma unroll
       for (int s = 0; s < 8; ++s) pb[s] = (bf16)cur[mt][rr + s];
+      const int vrow = 16 * kc + 4 * (G >> 1) + j4;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
-        const bf16x8 a =
-            *reinterpret_cast<const bf16x8*>(&Vt[buf][(32 * dt + c32) * VSTR + 16 * kc + 8 * g]);
-        oacc[dt] = mfma32(a, pb, oacc[dt]);
+        const bf16* vp = &Vs[buf][vrow * VSTR + 32 * dt + 16 * (G & 1) + 4 * m4];
+        oacc[dt] = mfma32(join(read_tr(vp), read_tr(vp + 8 * VSTR)), pb, oacc[dt]);
       }
     }
   };
@@ -267,13 +256,13 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     float* __restrict__ stat, int H, int T_, KVariant lo, KVariant hi,
     const int32_t* __restrict__ guard) {
   __shared__ __attribute__((aligned(16))) bf16 Ks[2][FBN * KSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Vt[2][HD * VSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[2][FBN * VSTR];
   if (LO == HI || guard_in_range(guard))
     fwd_body<LO & 3, (LO & 4) != 0, (LO & 8) != 0, (LO >> 4)>(q, k, v, sink, o, o_precise, stat,
-                                                              H, T_, lo, Ks, Vt);
+                                                              H, T_, lo, Ks, Vs);
   else
     fwd_body<HI & 3, (HI & 4) != 0, (HI & 8) != 0, (HI >> 4)>(q, k, v, sink, o, o_precise, stat,
-                                                              H, T_, hi, Ks, Vt);
+                                                              H, T_, hi, Ks, Vs);
 }
 
 typedef void (*FwdFn)(const bf16*, const bf16*, const bf16*, const float*, bf16*, float*, float*,

@@ -40,6 +40,19 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+// Transposing LDS read (ds_read_b64_tr_b16): lane 4j+m of each 16-lane group
+// addresses 4 consecutive bf16 of row j; lane i of the group receives element
+// i%4 of the rows addressed by lanes i/4, i/4+4, i/4+8, i/4+12.
+__device__ __forceinline__ bf16x4 read_tr(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+}
+
+__device__ __forceinline__ bf16x8 join(bf16x4 a, bf16x4 b) {
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
 __device__ __forceinline__ void zero16(f32x16& a) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) a[r] = 0.0f;
