@@ -360,9 +360,9 @@ int32_t launch_bwd_mfma(const void* q, const void* k, const void* v, const float
   const int grid = B * H * ((T + BKN - 1) / BKN);
   BwdFn fn = pick_bwd(cfg_for(lo), guard != nullptr ? cfg_for(hi) : cfg_for(lo));
   if (fn == nullptr) return fail("attn_bwd: no MFMA kernel for this variant pair");
-  ProbeScope probe(ALGX_PROBE_ATTN_BWD, s);
-  fn<<<grid, NTHR, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)v, stat, di,
-                           (const bf16*)dout, dq_acc, (bf16*)dk, (bf16*)dv, T, lo, hi, guard);
+  launch_k(probe_for(ALGX_PROBE_ATTN_BWD), fn, dim3(grid), dim3(NTHR), s, (const bf16*)q,
+           (const bf16*)k, (const bf16*)v, stat, di, (const bf16*)dout, dq_acc, (bf16*)dk,
+           (bf16*)dv, T, lo, hi, guard);
   return check_launch("attn_bwd_mfma");
 }
 

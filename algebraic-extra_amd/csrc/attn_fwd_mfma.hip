@@ -285,9 +285,8 @@ int32_t launch_fwd_mfma(const void* q, const void* k, const void* v, const float
   const int grid = B * H * (T / FBM);
   FwdFn fn = pick_fwd(cfg_for(lo), guard != nullptr ? cfg_for(hi) : cfg_for(lo));
   if (fn == nullptr) return fail("attn_fwd: no MFMA kernel for this variant pair");
-  ProbeScope probe(ALGX_PROBE_ATTN_FWD, s);
-  fn<<<grid, 256, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)v, sink, (bf16*)o,
-                          o_precise, stat, H, T, lo, hi, guard);
+  launch_k(probe_for(ALGX_PROBE_ATTN_FWD), fn, dim3(grid), dim3(256), s, (const bf16*)q,
+           (const bf16*)k, (const bf16*)v, sink, (bf16*)o, o_precise, stat, H, T, lo, hi, guard);
   return check_launch("attn_fwd_mfma");
 }
 

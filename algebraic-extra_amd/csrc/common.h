@@ -1,6 +1,7 @@
 // Shared device helpers for the algx gfx950 kernels.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -27,17 +28,23 @@ int32_t fill_f32(float* p, int64_t n, float value, hipStream_t s);
 
 // Records the registered probe events around one kernel launch (see
 // algx_set_probe): construct just before the launch, destroy just after.
-class ProbeScope {
- public:
-  ProbeScope(int which, hipStream_t s);
-  ~ProbeScope();
-  ProbeScope(const ProbeScope&) = delete;
-  ProbeScope& operator=(const ProbeScope&) = delete;
-
- private:
-  bool active_;
-  hipStream_t stream_;
+// HIP events armed by algx_set_probe for one kernel. A probed launch hands
+// them to hipExtLaunchKernel, which records them as part of the kernel's own
+// dispatch: timing inserts no extra packets (and no cache fences) between
+// kernels, so the probed kernel runs as it does unprobed.
+struct Probe {
+  hipEvent_t start = nullptr, stop = nullptr;
+  bool active() const { return start != nullptr; }
 };
+Probe probe_for(int which);
+
+template <typename F, typename... Args>
+void launch_k(const Probe& p, F kernel, dim3 grid, dim3 block, hipStream_t s, Args... args) {
+  if (p.active())
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, s, p.start, p.stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
+}
 
 // ------------------------------------------------------------- scalar math
 __device__ __forceinline__ float to_f(float x) { return x; }

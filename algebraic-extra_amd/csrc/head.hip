@@ -441,13 +441,10 @@ extern "C" int32_t algx_head_fwd(const void* h, const void* E, const int32_t* ta
   // the vocabulary tiles is never met).
   if (int32_t rc = fill_f32(zt, N, 0.0f, s)) return rc;
   {
-    ProbeScope probe(ALGX_PROBE_HEAD_FWD, s);
-    if (kind == ALGX_HEAD_CE)
-      head_fwd_kernel<ALGX_HEAD_CE><<<grid, kThreads, 0, s>>>(
-          (const bf16*)h, (const bf16*)E, targets, zt, partial, N, d, V, log2n, inv_c, clamp);
-    else
-      head_fwd_kernel<ALGX_HEAD_ALG_CE><<<grid, kThreads, 0, s>>>(
-          (const bf16*)h, (const bf16*)E, targets, zt, partial, N, d, V, log2n, inv_c, clamp);
+    const Probe probe = probe_for(ALGX_PROBE_HEAD_FWD);
+    launch_k(probe, kind == ALGX_HEAD_CE ? head_fwd_kernel<ALGX_HEAD_CE> : head_fwd_kernel<ALGX_HEAD_ALG_CE>,
+             grid, dim3(kThreads), s, (const bf16*)h, (const bf16*)E, targets, zt, partial, N, d,
+             V, log2n, inv_c, clamp);
   }
   if (int32_t rc = check_launch("head_fwd")) return rc;
   const int nb = (N + 255) / 256;
@@ -485,22 +482,18 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
   for (int tok0 = 0; tok0 < N; tok0 += csize) {
     const int ntok = min(csize, N - tok0);
     dim3 gdz((ntok + BN - 1) / BN, (V + BM - 1) / BM);
-    ProbeScope probe_dz(ALGX_PROBE_HEAD_DZ, s);
-    if (kind == ALGX_HEAD_CE)
-      head_dz_kernel<ALGX_HEAD_CE><<<gdz, kThreads, 0, s>>>(hb, eb, targets, stat, scale, dz, ldz,
-                                                           tok0, ntok, d, V, log2n, inv_c, clamp);
-    else
-      head_dz_kernel<ALGX_HEAD_ALG_CE><<<gdz, kThreads, 0, s>>>(
-          hb, eb, targets, stat, scale, dz, ldz, tok0, ntok, d, V, log2n, inv_c, clamp);
+    launch_k(probe_for(ALGX_PROBE_HEAD_DZ),
+             kind == ALGX_HEAD_CE ? head_dz_kernel<ALGX_HEAD_CE> : head_dz_kernel<ALGX_HEAD_ALG_CE>,
+             gdz, dim3(kThreads), s, hb, eb, targets, stat, scale, dz, ldz, tok0, ntok, d, V, log2n,
+             inv_c, clamp);
     if (int32_t rc = check_launch("head_dz")) return rc;
     // dh[t][c] = sum_v dz[t][v] E[v][c]: A = dz (k-contiguous), B(n=c,k=v) = E stored [v][c].
     {
       const Operand A{dz, ldz, ntok, V};
       const Operand B{eb, d, d, V};
       dim3 gg((d + BN - 1) / BN, (ntok + BM - 1) / BM);
-      ProbeScope probe(ALGX_PROBE_HEAD_DH, s);
-      gemm_kernel<true, false, bf16, false><<<gg, kThreads, 0, s>>>(
-          A, B, (bf16*)dh + (int64_t)tok0 * d, d, ntok, d);
+      launch_k(probe_for(ALGX_PROBE_HEAD_DH), gemm_kernel<true, false, bf16, false>, gg,
+               dim3(kThreads), s, A, B, (bf16*)dh + (int64_t)tok0 * d, (int64_t)d, ntok, d);
       if (int32_t rc = check_launch("head_dh")) return rc;
     }
     // dE[v][c] (+)= sum_t dz[t][v] h[t][c]: A(m=v,k=t) = dz stored [t][v], B(n=c,k=t) = h [t][c].
@@ -508,11 +501,9 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
       const Operand A{dz, ldz, V, ntok};
       const Operand B{hb + (int64_t)tok0 * d, d, d, ntok};
       dim3 gg((d + BN - 1) / BN, (V + BM - 1) / BM);
-      ProbeScope probe(ALGX_PROBE_HEAD_DE, s);
-      if (tok0 == 0)
-        gemm_kernel<false, false, float, false><<<gg, kThreads, 0, s>>>(A, B, dE, d, V, d);
-      else
-        gemm_kernel<false, false, float, true><<<gg, kThreads, 0, s>>>(A, B, dE, d, V, d);
+      launch_k(probe_for(ALGX_PROBE_HEAD_DE),
+               tok0 == 0 ? gemm_kernel<false, false, float, false> : gemm_kernel<false, false, float, true>,
+               gg, dim3(kThreads), s, A, B, dE, (int64_t)d, V, d);
       if (int32_t rc = check_launch("head_dE")) return rc;
     }
   }

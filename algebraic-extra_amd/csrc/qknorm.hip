@@ -182,11 +182,13 @@ extern "C" int32_t algx_qknorm_fwd(const void* x, const float* gain, void* y, in
   if (y == nullptr) return fail("qknorm: null output");
   hipStream_t s = (hipStream_t)stream;
   const int nb = blocks_for(rows, dtype);
-  ProbeScope probe(ALGX_PROBE_QKNORM_FWD, s);
+  const Probe probe = probe_for(ALGX_PROBE_QKNORM_FWD);
   if (dtype == ALGX_BF16)
-    qknorm_fwd_kernel<bf16><<<nb, kThreads, 0, s>>>((const bf16*)x, gain, (bf16*)y, rows, eps);
+    launch_k(probe, qknorm_fwd_kernel<bf16>, dim3(nb), dim3(kThreads), s, (const bf16*)x, gain,
+             (bf16*)y, rows, eps);
   else
-    qknorm_fwd_kernel<float><<<nb, kThreads, 0, s>>>((const float*)x, gain, (float*)y, rows, eps);
+    launch_k(probe, qknorm_fwd_kernel<float>, dim3(nb), dim3(kThreads), s, (const float*)x, gain,
+             (float*)y, rows, eps);
   return check_launch("qknorm_fwd");
 }
 
@@ -208,13 +210,13 @@ extern "C" int32_t algx_qknorm_bwd(const void* x, const float* gain, const void*
   const int nb = blocks_for(rows, dtype);
   float* partial = (float*)workspace;
   {
-    ProbeScope probe(ALGX_PROBE_QKNORM_BWD, s);
+    const Probe probe = probe_for(ALGX_PROBE_QKNORM_BWD);
     if (dtype == ALGX_BF16)
-      qknorm_bwd_kernel<bf16><<<nb, kThreads, 0, s>>>((const bf16*)x, gain, (const bf16*)dy,
-                                                      (bf16*)dx, partial, rows, eps);
+      launch_k(probe, qknorm_bwd_kernel<bf16>, dim3(nb), dim3(kThreads), s, (const bf16*)x, gain,
+               (const bf16*)dy, (bf16*)dx, partial, rows, eps);
     else
-      qknorm_bwd_kernel<float><<<nb, kThreads, 0, s>>>((const float*)x, gain, (const float*)dy,
-                                                       (float*)dx, partial, rows, eps);
+      launch_k(probe, qknorm_bwd_kernel<float>, dim3(nb), dim3(kThreads), s, (const float*)x,
+               gain, (const float*)dy, (float*)dx, partial, rows, eps);
   }
   if (int32_t rc = check_launch("qknorm_bwd")) return rc;
   qknorm_gain_finish<<<kD, kThreads, 0, s>>>(partial, nb, dgain);

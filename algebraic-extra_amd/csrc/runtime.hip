@@ -8,27 +8,23 @@ namespace algx {
 namespace {
 thread_local std::string g_error;
 // Process-wide: frameworks launch backward passes from their own threads.
-struct Probe {
+struct ArmedProbe {
   int which = ALGX_PROBE_NONE;
   hipEvent_t start = nullptr;
   hipEvent_t stop = nullptr;
 };
 std::mutex g_probe_mu;
-Probe g_probe;
+ArmedProbe g_probe;
 }  // namespace
 
-ProbeScope::ProbeScope(int which, hipStream_t s) : active_(false), stream_(s) {
+Probe probe_for(int which) {
   std::lock_guard<std::mutex> lk(g_probe_mu);
+  Probe p;
   if (g_probe.which != ALGX_PROBE_NONE && g_probe.which == which) {
-    active_ = true;
-    hipEventRecord(g_probe.start, stream_);
+    p.start = g_probe.start;
+    p.stop = g_probe.stop;
   }
-}
-
-ProbeScope::~ProbeScope() {
-  if (!active_) return;
-  std::lock_guard<std::mutex> lk(g_probe_mu);
-  hipEventRecord(g_probe.stop, stream_);
+  return p;
 }
 
 void set_error(const std::string& msg) { g_error = msg; }

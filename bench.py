@@ -12,8 +12,9 @@ convention (bench_attention.py:50,65: fwd+bwd = 3.5 * 4*B*H*T^2*D/2).
 
 One JSON line is printed. Besides the contract keys it carries:
   roofline      the dominant kernel (attention backward) timed with HIP events
-                recorded around its launch on its own stream, against the
-                MI355X dense bf16 MFMA peak;
+                that libalgx records as part of that kernel's own dispatch
+                (hipExtLaunchKernel, on the stream it runs on) during the timed
+                steps, against the MI355X dense bf16 MFMA peak;
   cpu_baseline  the reference's dense algebraic attention restated in torch
                 CPU float32 (oracle/cpu_baseline.py) on a bounded sample;
   secondary     configs[3] attention (H=16), the fused LM head + loss at
@@ -55,7 +56,8 @@ def make_attention_inputs(B, H, T, D, seed, dev):
 
 
 class Probe:
-    """HIP events recorded by libalgx around one named kernel (algx_set_probe)."""
+    """HIP events that libalgx records with one named kernel's dispatch
+    (algx_set_probe): one (start, stop) pair per timed step."""
 
     def __init__(self, which, count):
         import torch
@@ -81,9 +83,21 @@ class Probe:
         return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
 
 
-def time_steps(step, steps, warmup, probe=None):
-    """Wall time per step over `steps` after `warmup`; probe armed per step."""
+SETTLE_S = 1.0   # untimed running before the warmup steps: GPU clocks settle
+
+
+def time_steps(step, steps, warmup, probe=None, settle_s=SETTLE_S):
+    """Wall time per step over `steps` after `warmup`; probe armed per step.
+
+    Before the `warmup` steps the step runs untimed for `settle_s` seconds,
+    so the timed steps see the GPU at its steady clocks rather than ramping
+    out of idle (a cold MI355X runs the first ~second of work measurably
+    slower)."""
     import torch
+    t_end = time.perf_counter() + settle_s
+    while time.perf_counter() < t_end:
+        step()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()

@@ -51,9 +51,11 @@ int32_t algx_version(void);
 int32_t algx_selftest_mfma32(const void* a, const void* bt, float* d, void* stream);
 
 /* Diagnostic without a reference counterpart, for benchmarks: while set, the
- * named kernel records the caller's HIP events `start` before and `stop` after
- * its launch, on the stream it is launched on (which = ALGX_PROBE_NONE clears).
- * The setting is process-wide (backward passes often run on another thread). */
+ * named kernel is launched with hipExtLaunchKernel and the caller's HIP events
+ * `start` and `stop` recorded as part of its dispatch, on the stream it runs
+ * on (which = ALGX_PROBE_NONE clears). No extra packets enter the stream, so a
+ * probed kernel runs as it does unprobed. The setting is process-wide
+ * (backward passes often run on another thread). */
 enum {
   ALGX_PROBE_NONE = 0,
   ALGX_PROBE_ATTN_FWD = 1,   /* main attention forward kernel                  */
