@@ -96,7 +96,8 @@ def time_steps(step, steps, warmup, probe=None, settle_s=SETTLE_S):
     import torch
     t_end = time.perf_counter() + settle_s
     while time.perf_counter() < t_end:
-        step()
+        for _ in range(8):       # back to back, as the timed steps run
+            step()
         torch.cuda.synchronize()
     for _ in range(warmup):
         step()
