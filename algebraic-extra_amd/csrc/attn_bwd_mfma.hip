@@ -104,6 +104,7 @@ __device__ __forceinline__ void bwd_body(
   // Ones in the k rows 64, 65 of the extended V^T (dP's -di block).
   const bf16 one = (bf16)1.0f, zero = (bf16)0.0f;
   const bf16x8 ones = g == 0 ? bf16x8{one, one, zero, zero, zero, zero, zero, zero} : bf16x8{};
+  const float neg_g0 = g == 0 ? -1.0f : 0.0f;
   // K rows of the workgroup, row-major, for the dQ product; dS^T buffer 1
   // starts zeroed because the first tile's dQ step reads it.
 #pragma unroll
@@ -158,11 +159,12 @@ __device__ __forceinline__ void bwd_body(
       s = mfma32(*reinterpret_cast<const bf16x8*>(qrow + 16 * ks), kreg[ks], s);
       dp = mfma32(*reinterpret_cast<const bf16x8*>(grow + 16 * ks), vreg[ks], dp);
     }
-    const float dd = L.dd[buf][32 * mq + c32];
+    // Lanes g = 1 feed zeros; a multiply by a lane mask (not a branch around
+    // the load) keeps the tile in one basic block.
+    const float dd = L.dd[buf][32 * mq + c32] * neg_g0;
     const bf16 hi = (bf16)dd;
     const bf16 lo = (bf16)(dd - (float)hi);
-    const bf16x8 aext = g == 0 ? bf16x8{-hi, -lo, zero, zero, zero, zero, zero, zero} : bf16x8{};
-    dp = mfma32(aext, ones, dp);
+    dp = mfma32(bf16x8{hi, lo, zero, zero, zero, zero, zero, zero}, ones, dp);
   };
   // p, ds of half mq -> bf16 k-slot packs (two 16-query chunks each). Only
   // tiles that cross the diagonal (diag_tag = true_type) evaluate the mask.

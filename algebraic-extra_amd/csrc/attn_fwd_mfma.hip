@@ -204,12 +204,32 @@ __device__ __forceinline__ void fwd_body(
 
   auto visible = [&](int kb) { return kb < nkb && kb * FBN <= qw + 31; };
   auto step = [&](int kb, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
-    if (visible(kb + 1)) scores(kb + 1, nxt);
-    if (visible(kb)) {
-      if (kb * FBN + FBN - 1 > qw)
-        consume(std::true_type{}, kb, cur);
-      else
-        consume(std::false_type{}, kb, cur);
+    const bool vis_next = visible(kb + 1), vis = visible(kb);
+    const bool diag = kb * FBN + FBN - 1 > qw;
+    if (vis_next && vis && !diag) {
+      // Common case in one basic block, with the next tile's score MFMAs
+      // and this tile's PV MFMAs spread through the weight math (one MFMA
+      // per 20, then per 8, VALU operations) instead of issued back to back.
+      scores(kb + 1, nxt);
+      consume(std::false_type{}, kb, cur);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 20, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+      }
+    } else {
+      if (vis_next) scores(kb + 1, nxt);
+      if (vis) {
+        if (diag)
+          consume(std::true_type{}, kb, cur);
+        else
+          consume(std::false_type{}, kb, cur);
+      }
     }
     const int t = my_tile(kb);
     if (t < nkb) lstore(kloader ? (kb & 1) : ((kb + 1) & 1));
