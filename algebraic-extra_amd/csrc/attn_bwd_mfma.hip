@@ -124,28 +124,25 @@ __device__ __forceinline__ void bwd_body(
     zero16(dva[dt]);
   }
 
-  // Tile loader: thread t moves Q_s and dO row t/8, d 8(t%8) .. +7; threads
-  // 0..63 also move stat and di of query t.
+  // Tile loader: thread t moves Q_s and dO row t/8, d 8(t%8) .. +7.
   const int lrow = tid >> 3, lcol = 8 * (tid & 7);
   bf16x8 preq, preg;
   float pst = 0.0f, pdi = 0.0f;
   const int qt0 = key0 / BQ, nqt = T_ / BQ;
+  // Every wave moves stat and di of query `lane` (the same values), which
+  // keeps the loop free of branches.
   auto gload = [&](int qt) {
     const int64_t off = base + (int64_t)(qt * BQ + lrow) * HD + lcol;
     preq = *reinterpret_cast<const bf16x8*>(q + off);
     preg = *reinterpret_cast<const bf16x8*>(dout + off);
-    if (tid < BQ) {
-      pst = stat[rbase + qt * BQ + tid];
-      pdi = di[rbase + qt * BQ + tid];
-    }
+    pst = stat[rbase + qt * BQ + lane];
+    pdi = di[rbase + qt * BQ + lane];
   };
   auto lstore = [&](int buf) {
     *reinterpret_cast<bf16x8*>(&L.q[buf][lrow * RSTR + lcol]) = preq;
     *reinterpret_cast<bf16x8*>(&L.g[buf][lrow * RSTR + lcol]) = preg;
-    if (tid < BQ) {
-      L.st[buf][tid] = stat_pow ? powN<L2N>(pst, log2n) : pst;
-      L.dd[buf][tid] = pdi;
-    }
+    L.st[buf][lane] = stat_pow ? powN<L2N>(pst, log2n) : pst;
+    L.dd[buf][lane] = pdi;
   };
 
   // S and dP - di of query half mq: acc[r] <-> query 32mq + 8(r/4) + 4g + r%4, key kcol.
