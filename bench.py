@@ -114,11 +114,12 @@ def time_steps(step, steps, warmup, probe=None, settle_s=SETTLE_S):
     return dt
 
 
-def bench_attention(B, H, T, D, steps, warmup, dev):
+def bench_attention(B, H, T, D, steps, warmup, dev, kind="asinh"):
     import torch
     from algebraic_amd.kernels import flash_attention
     q, k, v, do = make_attention_inputs(B, H, T, D, 1, dev)
-    kw = dict(kind="asinh", n=16, c=8.0, range_guard=True)
+    kw = (dict(kind="asinh", n=16, c=8.0, range_guard=True) if kind == "asinh"
+          else dict(kind="softmax"))
 
     def step():
         o = flash_attention(q, k, v, **kw)
@@ -277,11 +278,17 @@ def main():
     }
     if not args.no_secondary:
         a16 = bench_attention(8, 16, T, D, max(5, args.steps // 2), 2, dev)
+        asm = bench_attention(B, H, T, D, max(5, args.steps // 2), 2, dev, kind="softmax")
         line["secondary"] = {
             "attn_h16": {"workload": "configs[3] attention B=8,H=16,T=2048,D=64",
                          "ms_per_step": round(a16["ms_per_step"], 4),
                          "tflops": round(a16["tflops"], 2),
                          "frac": round(a16["tflops"] / PEAK_BF16_TFLOPS, 4)},
+            "attn_softmax": {"workload": "softmax comparison arm at configs[1] (kind='softmax', "
+                                         "bench_attention.py:75-76)",
+                             "ms_per_step": round(asm["ms_per_step"], 4),
+                             "tflops": round(asm["tflops"], 2),
+                             "frac": round(asm["tflops"] / PEAK_BF16_TFLOPS, 4)},
             "fused_head": {k: (round(v, 4) if isinstance(v, float) else v)
                            for k, v in bench_head(5, 2, dev).items()},
             "qknorm": {k: (round(v, 4) if isinstance(v, float) else v)

@@ -110,3 +110,28 @@ def test_fused_head_alg_gradient_is_log_loss_gradient():
     assert rel_l2(got[2], th.grad.numpy()) < 1e-2
     assert rel_l2(got[3], te.grad.numpy()) < 1e-2
     np.testing.assert_allclose(got[1], np.exp(logp.detach().numpy()), rtol=2e-2, atol=2e-6)
+
+
+def test_fused_head_backward_over_token_chunks():
+    """N=12288 tokens at V=50304 spill the bf16 logit-gradient scratch past one
+    chunk (~1 GiB): the backward then runs two token chunks, the second
+    accumulating dE. Checked against dense float32 math on the GPU: the
+    objective mean(1 - p_t) (algebraic.py:243-245) and, as the reference's
+    custom VJP returns, the gradient of the mean NLL of
+    log_softmax(n asinh(z/c)) (the clamp is inactive at these logits)."""
+    N, d, V, n, c = 12288, 64, 50304, 8, 2.0
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    h = torch.randn((N, d), device=DEV, generator=gen).bfloat16()
+    e = (0.02 * torch.randn((V, d), device=DEV, generator=gen)).bfloat16()
+    t = torch.randint(0, V, (N,), device=DEV, generator=gen)
+    th, te = h.clone().requires_grad_(True), e.clone().requires_grad_(True)
+    obj, _ = fused_head(th, te, t, kind="alg_ce", n=n, c=c)
+    obj.backward()
+    rh, re = h.float().requires_grad_(True), e.float().requires_grad_(True)
+    logp = torch.log_softmax(n * torch.asinh((rh @ re.T) / c), -1).gather(1, t[:, None])
+    ref = float((1.0 - logp.exp()).mean())
+    (-logp.mean()).backward()
+    torch.cuda.synchronize()
+    assert abs(float(obj) - ref) <= 2e-4 + 2e-3 * abs(ref)
+    assert rel_l2(th.grad, rh.grad) <= 1e-2
+    assert rel_l2(te.grad, re.grad) <= 1e-2
