@@ -119,20 +119,23 @@ class _FlashFn(torch.autograd.Function):
         if plan.high is not None:
             words = _lib.query("algx_attn_guard_words")
             guard = torch.empty(words, dtype=torch.int32, device=dev)
-        # q_s = cast(q * scale) (flash.py:833), plus the guard word when guarded.
+        # One call: q_s = cast(q * scale) (flash.py:833), the guard word when
+        # guarded (:834-849) and the forward (:853-856).
         q_s = torch.empty_like(q)
-        _lib.call("algx_attn_prepare", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
-                  _lib.ptr(q_s), _lib.ptr(guard), B, H, T, D, dt, plan.q_scale, plan.bound,
-                  plan.vmax, st)
         o = torch.empty_like(q)
         stat = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         precise = plan.low.precise_output or (plan.high is not None and plan.high.precise_output)
         o_precise = torch.empty(q.shape, dtype=torch.float32, device=dev) if precise else None
+        ws = None
+        if guard is not None:
+            ws = torch.empty(_lib.query("algx_attn_forward_workspace_bytes", B, H, T, D),
+                             dtype=torch.uint8, device=dev)
         lo = _c_variant(plan.low)
         hi = _c_variant(plan.high) if plan.high is not None else None
-        _lib.call("algx_attn_fwd", _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
-                  _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat), B, H, T, D, dt, lo, hi,
-                  _lib.ptr(guard), st)
+        _lib.call("algx_attn_forward", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
+                  _lib.ptr(q_s), _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat),
+                  _lib.ptr(guard), _lib.ptr(ws), B, H, T, D, dt, plan.q_scale, plan.bound,
+                  plan.vmax, lo, hi, st)
         ctx.plan = plan
         ctx.save_for_backward(q_s, k, v, sink, o, o_precise, stat, guard)
         return o

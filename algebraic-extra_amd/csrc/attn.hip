@@ -94,6 +94,53 @@ extern "C" int32_t algx_attn_fwd(const void* q, const void* k, const void* v, co
   return 0;
 }
 
+extern "C" int64_t algx_attn_forward_workspace_bytes(int32_t B, int32_t H, int32_t T,
+                                                     int32_t D) {
+  (void)D;
+  if (B <= 0 || H <= 0 || T <= 0) return 0;
+  return fwd_fused_partials(B, H, T) * 3 * (int64_t)sizeof(float);
+}
+
+extern "C" int32_t algx_attn_forward(const void* q, const void* k, const void* v,
+                                     const float* sink, void* q_s, void* o, float* o_precise,
+                                     float* stat, int32_t* guard, void* workspace, int32_t B,
+                                     int32_t H, int32_t T, int32_t D, int32_t dtype,
+                                     float q_scale, float bound, float vmax,
+                                     const algx_attn_variant* low,
+                                     const algx_attn_variant* high, void* stream) {
+  if (int32_t rc = check_shape(B, H, T, D, dtype)) return rc;
+  KVariant kl{}, kh{};
+  if (int32_t rc = to_kvar(low, kl, "low")) return rc;
+  if (guard != nullptr) {
+    if (int32_t rc = to_kvar(high, kh, "high")) return rc;
+  } else {
+    kh = kl;
+  }
+  if ((int64_t)B * H * T == 0) return 0;
+  if (q == nullptr || k == nullptr || v == nullptr || q_s == nullptr || o == nullptr ||
+      stat == nullptr)
+    return fail("attn_forward: null pointer");
+  if ((kl.precise || (guard != nullptr && kh.precise)) && o_precise == nullptr)
+    return fail("attn_forward: precise-output variant needs o_precise");
+  hipStream_t s = (hipStream_t)stream;
+  if (mfma_supported(T, D, dtype) && !force_generic()) {
+    if (guard != nullptr && workspace == nullptr)
+      return fail("attn_forward: the guard needs the workspace");
+    return launch_fwd_fused(q, k, v, sink, q_s, o, o_precise, stat, guard, (float*)workspace, B,
+                            H, T, q_scale, bound, vmax, kl, kh, s);
+  }
+  if (int32_t rc = launch_prepare(q, k, v, sink, q_s, guard, B, H, T, D, dtype, q_scale, bound,
+                                  vmax, s))
+    return rc;
+  if (int32_t rc = launch_fwd_generic(q_s, k, v, sink, o, o_precise, stat, B, H, T, D, dtype, kl,
+                                      guard, 1, s))
+    return rc;
+  if (guard != nullptr)
+    return launch_fwd_generic(q_s, k, v, sink, o, o_precise, stat, B, H, T, D, dtype, kh, guard,
+                              0, s);
+  return 0;
+}
+
 extern "C" int64_t algx_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t T, int32_t D) {
   const int64_t rows = (int64_t)B * H * T;
   const int64_t acc = rows * D * (int64_t)sizeof(float);

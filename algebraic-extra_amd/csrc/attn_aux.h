@@ -10,6 +10,9 @@ int32_t guard_words();
 int32_t launch_prepare(const void* q, const void* k, const void* v, const float* sink, void* q_s,
                        int32_t* guard, int B, int H, int T, int D, int dtype, float q_scale,
                        float bound, float vmax, hipStream_t s);
+// Guard word from `nblocks` triples of partial maxima (|q_s|^2, |k|^2, |v|).
+int32_t launch_guard_finish(const float* partial, int nblocks, const float* sink, int H,
+                            float bound, float vmax, int32_t* guard, hipStream_t s);
 int32_t launch_bwd_pre(const void* dout, const void* o, const float* o_precise,
                        const float* stat, const float* sink, float* di, float* dq_acc,
                        float* dsink, int B, int H, int T, int D, int dtype, const KVariant& low,
@@ -37,6 +40,15 @@ int32_t launch_fwd_mfma(const void* q_s, const void* k, const void* v, const flo
                         void* o, float* o_precise, float* stat, int B, int H, int T,
                         const KVariant& lo, const KVariant& hi, const int32_t* guard,
                         hipStream_t s);
+// Pre-scale, guard and forward in one pass over q (MFMA shapes): the low
+// variant runs over the whole grid writing q_s and, guarded, one triple of
+// partial maxima per workgroup (fwd_fused_partials of them); the guard word
+// follows, then a high-variant launch that returns at once when in range.
+int64_t fwd_fused_partials(int B, int H, int T);
+int32_t launch_fwd_fused(const void* q, const void* k, const void* v, const float* sink,
+                         void* q_s, void* o, float* o_precise, float* stat, int32_t* guard,
+                         float* partial, int B, int H, int T, float q_scale, float bound,
+                         float vmax, const KVariant& lo, const KVariant& hi, hipStream_t s);
 int32_t launch_bwd_mfma(const void* q_s, const void* k, const void* v, const float* stat,
                         const float* di, const void* dout, float* dq_acc, void* dk, void* dv,
                         int B, int H, int T, const KVariant& lo, const KVariant& hi,

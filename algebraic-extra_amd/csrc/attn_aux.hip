@@ -266,8 +266,13 @@ int32_t launch_prepare(const void* q, const void* k, const void* v, const float*
   }
 #undef GUARD_CASE
   if (int32_t rc = check_launch("attn_guard_partial")) return rc;
+  return launch_guard_finish(partial, (int)nb, sink, H, bound, vmax, guard, s);
+}
+
+int32_t launch_guard_finish(const float* partial, int nblocks, const float* sink, int H,
+                            float bound, float vmax, int32_t* guard, hipStream_t s) {
   const double b101 = (double)bound / 1.01;
-  guard_finish_kernel<<<1, 256, 0, s>>>(partial, (int)nb, sink, H, (float)(b101 * b101),
+  guard_finish_kernel<<<1, 256, 0, s>>>(partial, nblocks, sink, H, (float)(b101 * b101),
                                         (float)b101, vmax, guard);
   return check_launch("attn_guard_finish");
 }

@@ -14,9 +14,9 @@
 //
 // dS^T goes to LDS once ([key][query], 8-byte stores), and each wave then
 // forms a 16-query x 32-d block of the tile's dQ over all 256 keys with
-// v_mfma_f32_16x16x32_bf16 (dS and K both read through transposing reads) and
-// adds it to a float32 accumulator with no-return atomics: one add per
-// element per 256 keys.
+// v_mfma_f32_16x16x32_bf16 (dS through transposing reads, K from a K^T copy
+// in LDS with 16-byte reads) and adds it to a float32 accumulator with
+// no-return atomics: one add per element per 256 keys.
 //
 // Pipelining: Q_s/dO/stat/di tiles and dS^T are double-buffered in LDS, so a
 // tile needs one barrier. The dQ of tile t-1 is formed while tile t's
@@ -33,7 +33,8 @@ constexpr int BKN = 256;   // keys per workgroup
 constexpr int BQ = 64;     // queries per tile
 constexpr int NWAVE = 8;
 constexpr int NTHR = 64 * NWAVE;
-constexpr int RSTR = 72;   // LDS row stride (bf16) of the Q_s, dO, K and dS^T tiles
+constexpr int RSTR = 72;   // LDS row stride (bf16) of the Q_s, dO and dS^T tiles
+constexpr int KTR = BKN + 8;  // LDS row stride of K^T [d][key]
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -66,7 +67,7 @@ struct BwdLds {
   float st[2][BQ];          // statistic (or its row factor)
   float dd[2][BQ];          // di
   bf16 dst[2][BKN * RSTR];  // dS^T [key][query]
-  bf16 k[BKN * RSTR];       // K rows of the workgroup [key][d]
+  bf16 kt[HD * KTR];        // K^T of the workgroup [d][key]
 };
 
 template <int MODE, bool FAST, bool BOUNDED, int L2N>
@@ -105,15 +106,17 @@ __device__ __forceinline__ void bwd_body(
   const bf16 one = (bf16)1.0f, zero = (bf16)0.0f;
   const bf16x8 ones = g == 0 ? bf16x8{one, one, zero, zero, zero, zero, zero, zero} : bf16x8{};
   const float neg_g0 = g == 0 ? -1.0f : 0.0f;
-  // K rows of the workgroup, row-major, for the dQ product; dS^T buffer 1
-  // starts zeroed because the first tile's dQ step reads it.
+  // K^T of the workgroup's keys for the dQ product (8 lanes share a key row,
+  // so the global reads coalesce); dS^T buffer 1 starts zeroed because the
+  // first tile's dQ step reads it.
 #pragma unroll
   for (int i = 0; i < BKN * HD / 8 / NTHR; ++i) {
     const int c = tid + NTHR * i, row = c >> 3, col = 8 * (c & 7);
     const bf16x8 val =
         key0 + row < T_ ? *reinterpret_cast<const bf16x8*>(k + base + (int64_t)(key0 + row) * HD + col)
                         : bf16x8{};
-    *reinterpret_cast<bf16x8*>(&L.k[row * RSTR + col]) = val;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) L.kt[(col + e) * KTR + row] = val[e];
     *reinterpret_cast<bf16x8*>(&L.dst[1][row * RSTR + col]) = bf16x8{};
   }
 
@@ -222,17 +225,14 @@ __device__ __forceinline__ void bwd_body(
   auto dq_tile = [&](int qt, int buf) {
     const int qr = 16 * (w & 3), dc = 32 * (w >> 2);
     f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
-    // Two k-steps per loop trip: a full unroll lets the scheduler hoist all
-    // 48 operand reads and spill.
-#pragma unroll 2
+#pragma unroll
     for (int kk = 0; kk < BKN / 32; ++kk) {
       const int krow = 32 * kk + 8 * G + j4;
       const bf16x8 a = join(read_tr(&L.dst[buf][krow * RSTR + qr + 4 * m4]),
                             read_tr(&L.dst[buf][(krow + 4) * RSTR + qr + 4 * m4]));
-      const bf16x8 b0 = join(read_tr(&L.k[krow * RSTR + dc + 4 * m4]),
-                             read_tr(&L.k[(krow + 4) * RSTR + dc + 4 * m4]));
-      const bf16x8 b1 = join(read_tr(&L.k[krow * RSTR + dc + 16 + 4 * m4]),
-                             read_tr(&L.k[(krow + 4) * RSTR + dc + 16 + 4 * m4]));
+      const bf16* kcol = &L.kt[(dc + i16) * KTR + 32 * kk + 8 * G];
+      const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(kcol);
+      const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(kcol + 16 * KTR);
       acc0 = mfma16(a, b0, acc0);
       acc1 = mfma16(a, b1, acc1);
     }

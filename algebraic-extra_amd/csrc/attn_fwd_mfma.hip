@@ -28,8 +28,8 @@ template <int MODE, bool FAST, bool BOUNDED, int L2N>
 __device__ __forceinline__ void fwd_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
-    float* __restrict__ stat, int H, int T_, const KVariant& var, bf16 (*Ks)[FBN * KSTR],
-    bf16 (*Vs)[FBN * VSTR]) {
+    float* __restrict__ stat, int H, int T_, const KVariant& var, const FwdPrep& prep,
+    bf16 (*Ks)[FBN * KSTR], bf16 (*Vs)[FBN * VSTR], float (*red)[4]) {
   const int nheads = gridDim.x / (T_ / FBM);
   int bh, qb;
   map_block(blockIdx.x, nheads, T_ / FBM, true, bh, qb);
@@ -47,6 +47,62 @@ __device__ __forceinline__ void fwd_body(
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
       qreg[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks);
+  }
+  if (prep.q_s != nullptr) {
+    // Fused pre-scale: `q` is the raw query; q_s = cast(q * scale)
+    // (flash.py:833) is formed in registers and written once for the
+    // backward. With a partial buffer the workgroup also reduces the range
+    // guard's maxima (flash.py:841-849): |q_s|^2 over its 128 query rows and
+    // |k|^2, |v| over the 128 key rows of its diagonal block, so the grid
+    // covers every row once. NaN becomes +inf so that it fails the guard.
+    bf16* qsp = prep.q_s + base + (int64_t)qrow * HD + 8 * g;
+    float sq = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8 x = qreg[ks];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = (bf16)((float)x[e] * prep.q_scale);
+        const float f = (float)x[e];
+        sq = __builtin_fmaf(f, f, sq);
+      }
+      qreg[ks] = x;
+      *reinterpret_cast<bf16x8*>(qsp + 16 * ks) = x;
+    }
+    if (prep.partial != nullptr) {
+      auto nan_to_inf = [](float x) { return x != x ? __builtin_inff() : x; };
+      sq = nan_to_inf(sq + __shfl_xor(sq, 32, 64));
+      const int64_t krow = base + (int64_t)(q0 + (tid >> 1)) * HD + 32 * (tid & 1);
+      float sk = 0.0f, mv = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const bf16x8 kx = *reinterpret_cast<const bf16x8*>(k + krow + 8 * c);
+        const bf16x8 vx = *reinterpret_cast<const bf16x8*>(v + krow + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float kf = (float)kx[e];
+          sk = __builtin_fmaf(kf, kf, sk);
+          mv = __builtin_fmaxf(mv, nan_to_inf(__builtin_fabsf((float)vx[e])));
+        }
+      }
+      sk = nan_to_inf(sk + __shfl_xor(sk, 1, 64));
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) {
+        sq = __builtin_fmaxf(sq, __shfl_xor(sq, m, 64));
+        sk = __builtin_fmaxf(sk, __shfl_xor(sk, m, 64));
+        mv = __builtin_fmaxf(mv, __shfl_xor(mv, m, 64));
+      }
+      if (lane == 0) {
+        red[0][w] = sq;
+        red[1][w] = sk;
+        red[2][w] = mv;
+      }
+      __syncthreads();
+      if (tid < 3)
+        prep.partial[(int64_t)blockIdx.x * 3 + tid] =
+            __builtin_fmaxf(__builtin_fmaxf(red[tid][0], red[tid][1]),
+                            __builtin_fmaxf(red[tid][2], red[tid][3]));
+    }
   }
 
   const bool has_sink = sink != nullptr;
@@ -267,26 +323,30 @@ __device__ __forceinline__ void fwd_body(
   if (g == 0) stat[(int64_t)bh * T_ + qrow] = final_stat(var, m_row, l_tot);
 }
 
-// One launch per call: the guard word (if any) picks the low or the high
-// variant for the whole grid, mirroring lax.cond(in_range, low, high).
+// The guard word (if any) picks the low or the high variant for the whole
+// grid, mirroring lax.cond(in_range, low, high). A launch with prep.skip set
+// is the high half of the fused call: it does nothing when that guard word
+// says in range.
 template <int LO, int HI>
 __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
     float* __restrict__ stat, int H, int T_, KVariant lo, KVariant hi,
-    const int32_t* __restrict__ guard) {
+    const int32_t* __restrict__ guard, FwdPrep prep) {
   __shared__ __attribute__((aligned(16))) bf16 Ks[2][FBN * KSTR];
   __shared__ __attribute__((aligned(16))) bf16 Vs[2][FBN * VSTR];
+  __shared__ float red[3][4];
+  if (prep.skip != nullptr && guard_in_range(prep.skip)) return;
   if (LO == HI || guard_in_range(guard))
     fwd_body<LO & 3, (LO & 4) != 0, (LO & 8) != 0, (LO >> 4)>(q, k, v, sink, o, o_precise, stat,
-                                                              H, T_, lo, Ks, Vs);
+                                                              H, T_, lo, prep, Ks, Vs, red);
   else
     fwd_body<HI & 3, (HI & 4) != 0, (HI & 8) != 0, (HI >> 4)>(q, k, v, sink, o, o_precise, stat,
-                                                              H, T_, hi, Ks, Vs);
+                                                              H, T_, hi, prep, Ks, Vs, red);
 }
 
 typedef void (*FwdFn)(const bf16*, const bf16*, const bf16*, const float*, bf16*, float*, float*,
-                      int, int, KVariant, KVariant, const int32_t*);
+                      int, int, KVariant, KVariant, const int32_t*, FwdPrep);
 
 FwdFn pick_fwd(int cl, int ch) { ALGX_PICK_ALL(fwd_mfma_kernel) }
 
@@ -294,8 +354,7 @@ FwdFn pick_fwd(int cl, int ch) { ALGX_PICK_ALL(fwd_mfma_kernel) }
 }  // namespace mfma
 
 bool mfma_supported(int T, int D, int dtype) {
-  return dtype == ALGX_BF16 && D == mfma::HD && T >= mfma::FBM && T % mfma::FBM == 0 &&
-         T % mfma::BBN == 0;
+  return dtype == ALGX_BF16 && D == mfma::HD && T >= mfma::FBM && T % mfma::FBM == 0;
 }
 
 int32_t launch_fwd_mfma(const void* q, const void* k, const void* v, const float* sink, void* o,
@@ -306,8 +365,40 @@ int32_t launch_fwd_mfma(const void* q, const void* k, const void* v, const float
   FwdFn fn = pick_fwd(cfg_for(lo), guard != nullptr ? cfg_for(hi) : cfg_for(lo));
   if (fn == nullptr) return fail("attn_fwd: no MFMA kernel for this variant pair");
   launch_k(probe_for(ALGX_PROBE_ATTN_FWD), fn, dim3(grid), dim3(256), s, (const bf16*)q,
-           (const bf16*)k, (const bf16*)v, sink, (bf16*)o, o_precise, stat, H, T, lo, hi, guard);
+           (const bf16*)k, (const bf16*)v, sink, (bf16*)o, o_precise, stat, H, T, lo, hi, guard,
+           FwdPrep{});
   return check_launch("attn_fwd_mfma");
+}
+
+int64_t fwd_fused_partials(int B, int H, int T) {
+  return (int64_t)B * H * (T / mfma::FBM);
+}
+
+int32_t launch_fwd_fused(const void* q, const void* k, const void* v, const float* sink,
+                         void* q_s, void* o, float* o_precise, float* stat, int32_t* guard,
+                         float* partial, int B, int H, int T, float q_scale, float bound,
+                         float vmax, const KVariant& lo, const KVariant& hi, hipStream_t s) {
+  using namespace mfma;
+  const int grid = B * H * (T / FBM);
+  // Low variant over the whole grid, fused with the pre-scale and (guarded)
+  // the guard's partial maxima. On out-of-range inputs its outputs are
+  // overwritten by the high launch below.
+  FwdFn fn = pick_fwd(cfg_for(lo), cfg_for(lo));
+  if (fn == nullptr) return fail("attn_forward: no MFMA kernel for the low variant");
+  FwdPrep pre{(bf16*)q_s, q_scale, guard != nullptr ? partial : nullptr, nullptr};
+  launch_k(probe_for(ALGX_PROBE_ATTN_FWD), fn, dim3(grid), dim3(256), s, (const bf16*)q,
+           (const bf16*)k, (const bf16*)v, sink, (bf16*)o, o_precise, stat, H, T, lo, lo,
+           (const int32_t*)nullptr, pre);
+  if (int32_t rc = check_launch("attn_forward_low")) return rc;
+  if (guard == nullptr) return 0;
+  if (int32_t rc = launch_guard_finish(partial, grid, sink, H, bound, vmax, guard, s)) return rc;
+  FwdFn fh = pick_fwd(cfg_for(hi), cfg_for(hi));
+  if (fh == nullptr) return fail("attn_forward: no MFMA kernel for the high variant");
+  FwdPrep skip{nullptr, 0.0f, nullptr, guard};
+  launch_k(Probe{}, fh, dim3(grid), dim3(256), s, (const bf16*)q_s, (const bf16*)k,
+           (const bf16*)v, sink, (bf16*)o, o_precise, stat, H, T, hi, hi,
+           (const int32_t*)nullptr, skip);
+  return check_launch("attn_forward_high");
 }
 
 }  // namespace algx

@@ -11,14 +11,19 @@ constexpr int HD = 64;
 constexpr int FBM = 128, FBN = 64;
 constexpr int KSTR = 72;  // K tile row stride (bf16): 144 B rows
 constexpr int VSTR = 72;  // V^T tile row stride
-// backward tiles: 128 keys per workgroup (32 per wave), 64-query tiles
-constexpr int BBN = 128, BBM = 64;
-constexpr int QSTR = 72;    // Q_s / dO row stride (64 d)
-constexpr int QTSTR = 72;   // Q_s^T / dO^T row stride (64 q)
-constexpr int DSSTR = 136;  // dS row stride (128 keys)
-constexpr int KTSTR = 136;  // K^T row stride (128 keys)
 
 enum { MODE_SOFTMAX = 0, MODE_NOSHIFT = 1, MODE_SHIFT = 2 };
+
+// Extra work of a forward launch: q_s != null -> `q` is the raw query and the
+// kernel writes q_s = cast(q * q_scale); partial != null -> it also writes the
+// range guard's three partial maxima per workgroup; skip != null -> the launch
+// does nothing when that guard word says in range.
+struct FwdPrep {
+  bf16* q_s = nullptr;
+  float q_scale = 1.0f;
+  float* partial = nullptr;
+  const int32_t* skip = nullptr;
+};
 
 // s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt left unconstrained
 // (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4], lgkmcnt[11:8]).

@@ -110,6 +110,22 @@ int32_t algx_attn_fwd(const void* q_s, const void* k, const void* v, const float
                       int32_t D, int32_t dtype, const algx_attn_variant* low,
                       const algx_attn_variant* high, const int32_t* guard, void* stream);
 
+/* algx_attn_forward = algx_attn_prepare + algx_attn_fwd in one call
+ * (flash.py:823-856 as one unit): the pre-scale, the guard and the forward.
+ * For bf16, D = 64, T % 128 == 0 the forward kernel reads the raw q itself,
+ * writes q_s (for the backward) and, with a guard buffer, one triple of
+ * partial guard maxima per workgroup into `workspace`
+ * (algx_attn_forward_workspace_bytes; may be NULL when guard is NULL); the
+ * guard word follows, and a high-variant launch that does nothing when the
+ * word says in range completes lax.cond. Other shapes run the two calls. */
+int64_t algx_attn_forward_workspace_bytes(int32_t B, int32_t H, int32_t T, int32_t D);
+int32_t algx_attn_forward(const void* q, const void* k, const void* v, const float* sink,
+                          void* q_s, void* o, float* o_precise, float* stat, int32_t* guard,
+                          void* workspace, int32_t B, int32_t H, int32_t T, int32_t D,
+                          int32_t dtype, float q_scale, float bound, float vmax,
+                          const algx_attn_variant* low, const algx_attn_variant* high,
+                          void* stream);
+
 int64_t algx_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t T, int32_t D);
 /* dq is w.r.t. the unscaled q: dq = cast(cast(dq_s) * q_scale) as autodiff of
  * flash.py:833 gives; dsink (H,) float32 is w.r.t. the kernel-unit sink

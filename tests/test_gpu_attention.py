@@ -232,3 +232,55 @@ def test_benchmark_shape_properties(H):
     res = OA.flash_attention(to_np(qs), to_np(ks), to_np(vs), None, dtype="bf16", **kw)
     assert res.in_range
     assert_bf16(o[3:4, 5:6], res.o, what="o(head)")
+
+
+@pytest.mark.parametrize("tail", [False, True])
+def test_fused_forward_equals_prepare_then_forward(tail):
+    """algx_attn_forward (pre-scale and guard fused into the MFMA forward, high
+    variant behind the guard word) gives the same q_s, o, stat and guard
+    decision as algx_attn_prepare followed by algx_attn_fwd."""
+    from algebraic_amd.kernels.flash import _c_variant, make_variant
+
+    B, H, T, D = 2, 3, 512, 64
+    q, k, v = (x.to(DEV) for x in _rand((B, H, T, D), 91, n=3))
+    if tail:
+        q = torch.full_like(q, math.sqrt(1000.0))
+        k = q.clone()
+    sink = torch.tensor([0.25, -0.5, 0.0], device=DEV)
+    # The guarded pair flash_attention builds for n=16, c=8 (flash.py:834-856).
+    var = make_variant("asinh", 16, 8.0, seq_len=T)
+    low = var._replace(shift=False, inv_stat=True, bounded_scores=True)
+    high = var._replace(shift=True, inv_stat=False, fast_rho=False, bounded_scores=False,
+                        head_resident=False, precise_output=True)
+    lo, hi = _c_variant(low), _c_variant(high)
+    bound = min(16.0, var.clamp / 2)
+    q_scale, vmax = 1.0 / (8.0 * math.sqrt(D)), min(1e8, 1e37 / ((T + 1) * (2 * bound + 1) ** 16))
+    st = _lib.stream()
+    words = _lib.query("algx_attn_guard_words")
+    outs = []
+    for fused in (True, False):
+        guard = torch.zeros(words, dtype=torch.int32, device=DEV)
+        q_s, o = torch.empty_like(q), torch.empty_like(q)
+        stat = torch.empty((B, H, T), dtype=torch.float32, device=DEV)
+        o_precise = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+        if fused:
+            ws = torch.empty(_lib.query("algx_attn_forward_workspace_bytes", B, H, T, D),
+                             dtype=torch.uint8, device=DEV)
+            _lib.call("algx_attn_forward", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
+                      _lib.ptr(q_s), _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat),
+                      _lib.ptr(guard), _lib.ptr(ws), B, H, T, D, _lib.dtype_code(q.dtype),
+                      q_scale, bound, vmax, lo, hi, st)
+        else:
+            _lib.call("algx_attn_prepare", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
+                      _lib.ptr(q_s), _lib.ptr(guard), B, H, T, D, _lib.dtype_code(q.dtype),
+                      q_scale, bound, vmax, st)
+            _lib.call("algx_attn_fwd", _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
+                      _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat), B, H, T, D,
+                      _lib.dtype_code(q.dtype), lo, hi, _lib.ptr(guard), st)
+        torch.cuda.synchronize()
+        outs.append((int(guard[0].item()), q_s, o, stat))
+    (g1, qs1, o1, s1), (g2, qs2, o2, s2) = outs
+    assert g1 == g2 == (0 if tail else 1)
+    assert torch.equal(qs1, qs2)
+    assert torch.equal(o1, o2)
+    assert torch.equal(s1, s2)
