@@ -13,17 +13,22 @@
 // and the scaled bf16 logit gradient dz (fused_head.py:145) is written for a
 // chunk of tokens; dh = dz E and dE += dz^T h are then plain MFMA GEMMs over
 // that chunk (the reference also materialises dz and runs an XLA GEMM for dE).
+#include <cstdlib>
+
 #include "common.h"
 
 namespace algx {
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int LSTR = BK + 8;  // LDS row stride (bf16) of k-contiguous tiles: 144 B
-constexpr int TSTR = BM + 16;  // LDS row stride (bf16) of [k][mn] tiles: 288 B
-constexpr int kThreads = 256;
-constexpr int kVocabChunkTiles = 16;  // vocabulary tiles per forward workgroup
+constexpr int BM = 256, BN = 256, BK = 32;  // output tile and k stage of every GEMM
+constexpr int LSTR = BK + 8;   // LDS row stride (bf16) of k-contiguous tiles: 80 B
+constexpr int TSTR = BM + 16;  // LDS row stride (bf16) of [k][mn] tiles: 544 B
+constexpr int kThreads = 512;  // 8 waves: 2 (m) x 4 (n), 128 x 64 outputs per wave
+constexpr int TI = 4, TJ = 2;  // 32x32 MFMA tiles per wave along m and n
+constexpr int kStageElems = BM * LSTR > BK * TSTR ? BM * LSTR : BK * TSTR;
+constexpr int kChunks = BM * BK / 8 / kThreads;  // 16-byte chunks per thread per tile stage
+constexpr int kVocabChunkTiles = 8;  // vocabulary tiles per forward workgroup
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -38,49 +43,69 @@ struct Operand {
   int K;
 };
 
-// Stages one BM x BK tile of an operand into registers (zero outside).
+// Stages one 256 x 64 (mn x k) tile of an operand into registers (zero
+// outside): four 16-byte loads per thread.
+// Per-thread addressing of one operand tile (set once per output tile): the
+// thread's chunks of a 256 x BK (mn x k) stage.
+template <bool KC>
+struct TileAddr {
+  const bf16* base[kChunks];  // chunk address at k stage 0 (op.p when its mn is outside)
+  int koff[kChunks];          // k of the chunk within a stage
+  bool mn_in[kChunks];
+  __device__ __forceinline__ void init(const Operand& op, int mn0, int tid) {
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      if (KC) {
+        // [mn][k]: BK / 8 chunks per row.
+        const int id = tid + kThreads * c;
+        const int row = mn0 + id / (BK / 8);
+        koff[c] = (id % (BK / 8)) * 8;
+        mn_in[c] = row < op.rows;
+        base[c] = op.p + (mn_in[c] ? (int64_t)row * op.ld + koff[c] : 0);
+      } else {
+        // [k][mn]: kChunks consecutive k rows x 8 consecutive mn per thread.
+        const int kg = tid >> 5, mg = tid & 31;
+        const int mm = mn0 + 8 * mg;
+        koff[c] = kChunks * kg + c;
+        mn_in[c] = mm < op.rows;
+        base[c] = op.p + (mn_in[c] ? (int64_t)koff[c] * op.ld + mm : 0);
+      }
+    }
+  }
+};
+
 template <bool KC>
 struct TileLoader {
-  bf16x8 r[4];
-  __device__ __forceinline__ void load(const Operand& op, int mn0, int k0, int tid) {
-    if (KC) {
+  bf16x8 r[kChunks];
+  uint32_t ok;  // bit c: chunk c is inside the operand
+  // Branch-free: an out-of-range chunk reads the operand's first 16 bytes and
+  // is replaced by zeros when stored, so no wait for the load sits here.
+  __device__ __forceinline__ void load(const Operand& op, const TileAddr<KC>& ad, int k0) {
+    ok = 0;
+    const int64_t step = KC ? (int64_t)k0 : (int64_t)k0 * op.ld;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int id = tid + kThreads * c;
-        const int row = mn0 + (id >> 3), col = k0 + (id & 7) * 8;
-        if (row < op.rows && col < op.K)
-          r[c] = *reinterpret_cast<const bf16x8*>(op.p + (int64_t)row * op.ld + col);
-        else
-          r[c] = bf16x8{};
-      }
-    } else {
-      // 4 consecutive k rows x 8 consecutive m: unit = (k group kg, m group mg).
-      const int kg = tid >> 4, mg = tid & 15;
-      const int mm = mn0 + 8 * mg;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kk = k0 + 4 * kg + i;
-        if (kk < op.K && mm < op.rows)
-          r[i] = *reinterpret_cast<const bf16x8*>(op.p + (int64_t)kk * op.ld + mm);
-        else
-          r[i] = bf16x8{};
-      }
+    for (int c = 0; c < kChunks; ++c) {
+      const bool in = ad.mn_in[c] && k0 + ad.koff[c] < op.K;
+      ok |= in ? 1u << c : 0u;
+      r[c] = *reinterpret_cast<const bf16x8*>(in ? ad.base[c] + step : op.p);
     }
   }
   __device__ __forceinline__ void store(bf16* lds, int tid) const {
     if (KC) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < kChunks; ++c) {
         const int id = tid + kThreads * c;
-        *reinterpret_cast<bf16x8*>(lds + (id >> 3) * LSTR + (id & 7) * 8) = r[c];
+        *reinterpret_cast<bf16x8*>(lds + (id / (BK / 8)) * LSTR + (id % (BK / 8)) * 8) =
+            (ok >> c) & 1 ? r[c] : bf16x8{};
       }
     } else {
       // Kept as stored in memory, [k][mn]; the MFMA operand is read through
       // transposing LDS reads.
-      const int kg = tid >> 4, mg = tid & 15;
+      const int kg = tid >> 5, mg = tid & 31;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<bf16x8*>(lds + (4 * kg + i) * TSTR + 8 * mg) = r[i];
+      for (int i = 0; i < kChunks; ++i)
+        *reinterpret_cast<bf16x8*>(lds + (kChunks * kg + i) * TSTR + 8 * mg) =
+            (ok >> i) & 1 ? r[i] : bf16x8{};
     }
   }
 };
@@ -104,14 +129,15 @@ __device__ __forceinline__ bf16x8 operand(const bf16* tile, int mn0, int k0, int
   }
 }
 
-// acc[i][j][r] = C[m0 + 64wm + 32i + 8(r/4) + 4g + r%4][n0 + 64wn + 32j + c32]
+// Wave w = (wm, wn) = (w / 4, w % 4) owns outputs m0 + 128wm .. +127,
+// n0 + 64wn .. +63: acc.v[i][j][r] = C[m0 + 128wm + 32i + 8(r/4) + 4g + r%4][n0 + 64wn + 32j + c32].
 struct Acc {
-  f32x16 v[2][2];
+  f32x16 v[TI][TJ];
   __device__ __forceinline__ void zero() {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < TJ; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) v[i][j][r] = 0.0f;
   }
@@ -122,47 +148,64 @@ __device__ __forceinline__ void mma_stage(const bf16* As, const bf16* Bs, Acc& a
                                           int wn, int lane) {
 #pragma unroll
   for (int ks = 0; ks < BK / 16; ++ks) {
-    bf16x8 a[2], b[2];
+    bf16x8 a[TI], b[TJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) a[i] = operand<AKC>(As, 64 * wm + 32 * i, 16 * ks, lane);
+    for (int i = 0; i < TI; ++i) a[i] = operand<AKC>(As, 128 * wm + 32 * i, 16 * ks, lane);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) b[j] = operand<BKC>(Bs, 64 * wn + 32 * j, 16 * ks, lane);
+    for (int j = 0; j < TJ; ++j) b[j] = operand<BKC>(Bs, 64 * wn + 32 * j, 16 * ks, lane);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc.v[i][j] = mfma32(a[i], b[j], acc.v[i][j]);
+      for (int j = 0; j < TJ; ++j) acc.v[i][j] = mfma32(a[i], b[j], acc.v[i][j]);
   }
 }
 
-// Full-K product of one output tile with a double-buffered LDS pipeline.
+// Full-K product of one output tile: LDS double-buffered, global loads two
+// k stages ahead (two register sets, so a stage's HBM latency spans two
+// stages of MFMA work).
 template <bool AKC, bool BKC>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int m0, int n0,
                                           bf16* As, bf16* Bs, Acc& acc, int tid) {
-  const int w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
-  const int wm = w >> 1, wn = w & 1;
+  const int w = tid >> 6, lane = tid & 63;
+  const int wm = w >> 2, wn = w & 3;
   const int K = A.K;
   const int nk = (K + BK - 1) / BK;
-  TileLoader<AKC> la;
-  TileLoader<BKC> lb;
+  TileAddr<AKC> aa;
+  TileAddr<BKC> ab;
+  aa.init(A, m0, tid);
+  ab.init(B, n0, tid);
+  TileLoader<AKC> la0, la1;
+  TileLoader<BKC> lb0, lb1;
   acc.zero();
-  la.load(A, m0, 0, tid);
-  lb.load(B, n0, 0, tid);
+  // Every step issues the same loads (stage indices past the end are clamped
+  // to the last stage and never stored), so each wait before a store covers
+  // exactly the loads of the stage it stores.
+  const int klast = (nk - 1) * BK;
+  la0.load(A, aa, 0);
+  lb0.load(B, ab, 0);
+  la1.load(A, aa, min(BK, klast));
+  lb1.load(B, ab, min(BK, klast));
   __syncthreads();  // previous users of the LDS buffers are done
-  la.store(As, tid);
-  lb.store(Bs, tid);
+  la0.store(As, tid);
+  lb0.store(Bs, tid);
   __syncthreads();
-  for (int kk = 0; kk < nk; ++kk) {
+  // Stage kk sits in LDS buffer kk % 2; register set kk % 2 held it and is
+  // refilled with stage kk + 2 while stage kk + 1 waits in the other set.
+  auto step = [&](int kk, TileLoader<AKC>& la_cur, TileLoader<BKC>& lb_cur,
+                  TileLoader<AKC>& la_nxt, TileLoader<BKC>& lb_nxt) {
     const int buf = kk & 1;
+    la_cur.load(A, aa, min((kk + 2) * BK, klast));
+    lb_cur.load(B, ab, min((kk + 2) * BK, klast));
+    mma_stage<AKC, BKC>(As + buf * kStageElems, Bs + buf * kStageElems, acc, wm, wn, lane);
     if (kk + 1 < nk) {
-      la.load(A, m0, (kk + 1) * BK, tid);
-      lb.load(B, n0, (kk + 1) * BK, tid);
-    }
-    mma_stage<AKC, BKC>(As + buf * BM * LSTR, Bs + buf * BN * LSTR, acc, wm, wn, lane);
-    if (kk + 1 < nk) {
-      la.store(As + (buf ^ 1) * BM * LSTR, tid);
-      lb.store(Bs + (buf ^ 1) * BN * LSTR, tid);
+      la_nxt.store(As + (buf ^ 1) * kStageElems, tid);
+      lb_nxt.store(Bs + (buf ^ 1) * kStageElems, tid);
     }
     __syncthreads();
+  };
+  for (int kk = 0; kk < nk; kk += 2) {
+    step(kk, la0, lb0, la1, lb1);
+    if (kk + 1 < nk) step(kk + 1, la1, lb1, la0, lb0);
   }
 }
 
@@ -180,11 +223,11 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
     const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
     float* __restrict__ zt, float* __restrict__ partial, int N, int d, int V, int log2n,
     float inv_c, float clamp) {
-  __shared__ __attribute__((aligned(16))) bf16 As[2 * BM * LSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * BN * LSTR];
-  __shared__ float red_m[4][BN], red_l[4][BN];
+  __shared__ __attribute__((aligned(16))) bf16 As[2 * kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * kStageElems];
+  __shared__ float red_m[2][BN], red_l[2][BN];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w >> 2, wn = w & 3;
   const int n0 = blockIdx.x * BN;
   const int chunk = blockIdx.y;
   const int ntiles_v = (V + BM - 1) / BM;
@@ -192,10 +235,10 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
   const int t_end = min(ntiles_v, t_begin + kVocabChunkTiles);
   const Operand A{e, d, V, d};
   const Operand B{h, d, N, d};
-  int tok[2], tgt[2];
-  float m_st[2], l_st[2];
+  int tok[TJ], tgt[TJ];
+  float m_st[TJ], l_st[TJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < TJ; ++j) {
     tok[j] = n0 + 64 * wn + 32 * j + c32;
     tgt[j] = tok[j] < N ? targets[tok[j]] : -1;
     m_st[j] = -1e30f;
@@ -206,24 +249,24 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
     const int m0 = t * BM;
     gemm_tile<true, true>(A, B, m0, n0, As, Bs, acc, tid);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < TJ; ++j) {
       float tile_max = -1e30f;
       if (KIND == ALGX_HEAD_CE) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+            const int m = m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
             if (m < V) tile_max = __builtin_fmaxf(tile_max, acc.v[i][j][r]);
           }
       }
       const float m_new = __builtin_fmaxf(m_st[j], tile_max);
       float lsum = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+          const int m = m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
           const float z = acc.v[i][j][r];
           if (m == tgt[j]) zt[tok[j]] = z;
           float wgt;
@@ -243,9 +286,9 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
       }
     }
   }
-  // Merge the 4 partial states of each token: lane halves g and waves wm.
+  // Merge the 4 partial states of each token: lane halves g, then waves wm.
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < TJ; ++j) {
     float mo = __shfl_xor(m_st[j], 32, 64), lo = __shfl_xor(l_st[j], 32, 64);
     if (KIND == ALGX_HEAD_CE) {
       const float mm = __builtin_fmaxf(m_st[j], mo);
@@ -256,17 +299,15 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
       l_st[j] += lo;
     }
     if (g == 0) {
-      red_m[wm * 2 + j][64 * wn + c32] = m_st[j];
-      red_l[wm * 2 + j][64 * wn + c32] = l_st[j];
+      red_m[wm][64 * wn + 32 * j + c32] = m_st[j];
+      red_l[wm][64 * wn + 32 * j + c32] = l_st[j];
     }
   }
   __syncthreads();
   if (tid < BN) {
-    const int col = tid, jj = (col & 63) >> 5;  // column -> (wn, j, c32)
-    const int wnn = col >> 6, cc = col & 31;
-    const int slot = 64 * wnn + cc;
-    const float m_a = red_m[0 * 2 + jj][slot], l_a = red_l[0 * 2 + jj][slot];
-    const float m_b = red_m[1 * 2 + jj][slot], l_b = red_l[1 * 2 + jj][slot];
+    const int col = tid;
+    const float m_a = red_m[0][col], l_a = red_l[0][col];
+    const float m_b = red_m[1][col], l_b = red_l[1][col];
     float m_out, l_out;
     if (KIND == ALGX_HEAD_CE) {
       m_out = __builtin_fmaxf(m_a, m_b);
@@ -313,10 +354,10 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
     const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
     const float* __restrict__ stat, const float* __restrict__ scale, bf16* __restrict__ dz,
     int64_t ldz, int tok0, int ntok, int d, int V, int log2n, float inv_c, float clamp) {
-  __shared__ __attribute__((aligned(16))) bf16 As[2 * BM * LSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * BN * LSTR];
+  __shared__ __attribute__((aligned(16))) bf16 As[2 * kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * kStageElems];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w >> 2, wn = w & 3;
   const int n0 = blockIdx.x * BN;   // token offset inside the chunk
   const int m0 = blockIdx.y * BM;   // vocabulary offset
   const Operand A{e, d, V, d};
@@ -325,16 +366,16 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
   gemm_tile<true, true>(A, B, m0, n0, As, Bs, acc, tid);
   const float sc = scale[0];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < TJ; ++j) {
     const int tl = n0 + 64 * wn + 32 * j + c32;
     if (tl >= ntok) continue;
     const int tgt = targets[tok0 + tl];
     const float st = stat[tok0 + tl];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        const int mb = m0 + 64 * wm + 32 * i + 8 * q4 + 4 * g;
+        const int mb = m0 + 128 * wm + 32 * i + 8 * q4 + 4 * g;
         bf16x4 out;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -357,28 +398,35 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
   }
 }
 
-// Plain GEMM C[m][n] (+)= sum_k A(m,k) B(n,k) with float32 or bf16 output.
+// One GEMM of a grouped launch: C[m][n] (+)= sum_k A(m,k) B(n,k).
+struct GemmJob {
+  Operand A, B;
+  void* C;
+  int64_t ldc;
+  int M, N;
+  int tiles_n;  // output tiles along n
+};
+
 template <bool AKC, bool BKC, typename TOut, bool ACCUM>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(Operand A, Operand B, TOut* __restrict__ C,
-                                                        int64_t ldc, int M, int N) {
-  __shared__ __attribute__((aligned(16))) bf16 As[2 * BM * LSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * BN * LSTR];
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
-  const int wm = w >> 1, wn = w & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+__device__ __forceinline__ void gemm_job(const GemmJob& jb, int tile, bf16* As, bf16* Bs,
+                                         int tid) {
+  const int w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
+  const int wm = w >> 2, wn = w & 3;
+  const int m0 = (tile / jb.tiles_n) * BM, n0 = (tile % jb.tiles_n) * BN;
   Acc acc;
-  gemm_tile<AKC, BKC>(A, B, m0, n0, As, Bs, acc, tid);
+  gemm_tile<AKC, BKC>(jb.A, jb.B, m0, n0, As, Bs, acc, tid);
+  TOut* C = reinterpret_cast<TOut*>(jb.C);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < TJ; ++j) {
       const int n = n0 + 64 * wn + 32 * j + c32;
-      if (n >= N) continue;
+      if (n >= jb.N) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (m >= M) continue;
-        TOut* dst = C + (int64_t)m * ldc + n;
+        const int m = m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (m >= jb.M) continue;
+        TOut* dst = C + (int64_t)m * jb.ldc + n;
         if (ACCUM)
           *dst = from_f<TOut>(to_f(*dst) + acc.v[i][j][r]);
         else
@@ -387,12 +435,33 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Operand A, Operand B, TO
     }
 }
 
+// The backward's two products of a token chunk in one launch (the long-K dh
+// tiles first): dh[t][c] = sum_v dz[t][v] E[v][c] for blocks [0, n_dh), then
+// dE[v][c] (+)= sum_t dz[t][v] h[t][c].
+template <bool ACCUM>
+__global__ __launch_bounds__(kThreads) void head_grad_kernel(GemmJob dh, GemmJob de, int n_dh) {
+  __shared__ __attribute__((aligned(16))) bf16 As[2 * kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * kStageElems];
+  const int b = blockIdx.x;
+  if (b < n_dh)
+    gemm_job<true, false, bf16, false>(dh, b, As, Bs, threadIdx.x);
+  else
+    gemm_job<false, false, float, ACCUM>(de, b - n_dh, As, Bs, threadIdx.x);
+}
+
 int64_t vpad_of(int V) { return ((int64_t)V + BM - 1) / BM * BM; }
 
-// Token chunk of the backward: bounds the dz scratch to ~1 GiB.
+// Token chunk of the backward: bounds the bf16 dz scratch to 2 GiB (all
+// 16384 tokens of a 50304-word vocabulary in one chunk), or to
+// ALGX_HEAD_CHUNK_BYTES when that is set.
 int chunk_tokens(int N, int V) {
   const int64_t per_tok = vpad_of(V) * 2;
-  int64_t c = ((int64_t)1 << 30) / per_tok;
+  int64_t limit = (int64_t)2 << 30;
+  if (const char* env = std::getenv("ALGX_HEAD_CHUNK_BYTES")) {
+    const long long v = std::atoll(env);
+    if (v > 0) limit = v;
+  }
+  int64_t c = limit / per_tok;
   c = c / BN * BN;
   if (c < BN) c = BN;
   return (int)(c > N ? ((N + BN - 1) / BN) * BN : c);
@@ -488,24 +557,17 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
              inv_c, clamp);
     if (int32_t rc = check_launch("head_dz")) return rc;
     // dh[t][c] = sum_v dz[t][v] E[v][c]: A = dz (k-contiguous), B(n=c,k=v) = E stored [v][c].
-    {
-      const Operand A{dz, ldz, ntok, V};
-      const Operand B{eb, d, d, V};
-      dim3 gg((d + BN - 1) / BN, (ntok + BM - 1) / BM);
-      launch_k(probe_for(ALGX_PROBE_HEAD_DH), gemm_kernel<true, false, bf16, false>, gg,
-               dim3(kThreads), s, A, B, (bf16*)dh + (int64_t)tok0 * d, (int64_t)d, ntok, d);
-      if (int32_t rc = check_launch("head_dh")) return rc;
-    }
     // dE[v][c] (+)= sum_t dz[t][v] h[t][c]: A(m=v,k=t) = dz stored [t][v], B(n=c,k=t) = h [t][c].
-    {
-      const Operand A{dz, ldz, V, ntok};
-      const Operand B{hb + (int64_t)tok0 * d, d, d, ntok};
-      dim3 gg((d + BN - 1) / BN, (V + BM - 1) / BM);
-      launch_k(probe_for(ALGX_PROBE_HEAD_DE),
-               tok0 == 0 ? gemm_kernel<false, false, float, false> : gemm_kernel<false, false, float, true>,
-               gg, dim3(kThreads), s, A, B, dE, (int64_t)d, V, d);
-      if (int32_t rc = check_launch("head_dE")) return rc;
-    }
+    const int tn = (d + BN - 1) / BN;
+    const GemmJob jdh{Operand{dz, ldz, ntok, V}, Operand{eb, d, d, V},
+                      (bf16*)dh + (int64_t)tok0 * d, (int64_t)d, ntok, d, tn};
+    const GemmJob jde{Operand{dz, ldz, V, ntok}, Operand{hb + (int64_t)tok0 * d, d, d, ntok},
+                      dE, (int64_t)d, V, d, tn};
+    const int n_dh = ((ntok + BM - 1) / BM) * tn;
+    const int n_de = ((V + BM - 1) / BM) * tn;
+    launch_k(probe_for(ALGX_PROBE_HEAD_DE), tok0 == 0 ? head_grad_kernel<false> : head_grad_kernel<true>,
+             dim3(n_dh + n_de), dim3(kThreads), s, jdh, jde, n_dh);
+    if (int32_t rc = check_launch("head_grad")) return rc;
   }
   return 0;
 }

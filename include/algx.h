@@ -62,8 +62,8 @@ enum {
   ALGX_PROBE_ATTN_BWD = 2,   /* main attention backward kernel                 */
   ALGX_PROBE_HEAD_FWD = 3,   /* fused-head forward statistics kernel           */
   ALGX_PROBE_HEAD_DZ = 4,    /* fused-head backward logit-gradient kernel      */
-  ALGX_PROBE_HEAD_DH = 5,    /* fused-head dh GEMM                             */
-  ALGX_PROBE_HEAD_DE = 6,    /* fused-head dE GEMM                             */
+  ALGX_PROBE_HEAD_DH = 5,    /* unused: dh runs in the ALGX_PROBE_HEAD_DE launch */
+  ALGX_PROBE_HEAD_DE = 6,    /* fused-head dh + dE GEMM launch                 */
   ALGX_PROBE_QKNORM_FWD = 7,
   ALGX_PROBE_QKNORM_BWD = 8
 };
