@@ -14,6 +14,7 @@
 // chunk of tokens; dh = dz E and dE += dz^T h are then plain MFMA GEMMs over
 // that chunk (the reference also materialises dz and runs an XLA GEMM for dE).
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.h"
 
@@ -24,10 +25,15 @@ namespace {
 constexpr int BM = 256, BN = 256, BK = 32;  // output tile and k stage of every GEMM
 constexpr int LSTR = BK + 8;   // LDS row stride (bf16) of k-contiguous tiles: 80 B
 constexpr int TSTR = BM + 16;  // LDS row stride (bf16) of [k][mn] tiles: 544 B
-constexpr int kThreads = 512;  // 8 waves: 2 (m) x 4 (n), 128 x 64 outputs per wave
-constexpr int TI = 4, TJ = 2;  // 32x32 MFMA tiles per wave along m and n
+constexpr int NWM = 2, NWN = 4;               // waves along m and n
+constexpr int kThreads = 64 * NWM * NWN;
+constexpr int WTM = BM / NWM, WTN = BN / NWN;  // outputs per wave: 128 x 64
+constexpr int TI = WTM / 32, TJ = WTN / 32;    // 32x32 MFMA tiles per wave along m and n
 constexpr int kStageElems = BM * LSTR > BK * TSTR ? BM * LSTR : BK * TSTR;
 constexpr int kChunks = BM * BK / 8 / kThreads;  // 16-byte chunks per thread per tile stage
+static_assert(BM == BN && (BM / 8) * (kThreads / (BM / 8)) == kThreads &&
+                  kChunks * (kThreads / (BM / 8)) == BK,
+              "[k][mn] loader: BM/8 threads per k row group, kChunks k rows each");
 constexpr int kVocabChunkTiles = 8;  // vocabulary tiles per forward workgroup
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
@@ -64,7 +70,7 @@ struct TileAddr {
         base[c] = op.p + (mn_in[c] ? (int64_t)row * op.ld + koff[c] : 0);
       } else {
         // [k][mn]: kChunks consecutive k rows x 8 consecutive mn per thread.
-        const int kg = tid >> 5, mg = tid & 31;
+        const int kg = tid / (BM / 8), mg = tid % (BM / 8);
         const int mm = mn0 + 8 * mg;
         koff[c] = kChunks * kg + c;
         mn_in[c] = mm < op.rows;
@@ -101,7 +107,7 @@ struct TileLoader {
     } else {
       // Kept as stored in memory, [k][mn]; the MFMA operand is read through
       // transposing LDS reads.
-      const int kg = tid >> 5, mg = tid & 31;
+      const int kg = tid / (BM / 8), mg = tid % (BM / 8);
 #pragma unroll
       for (int i = 0; i < kChunks; ++i)
         *reinterpret_cast<bf16x8*>(lds + (kChunks * kg + i) * TSTR + 8 * mg) =
@@ -129,8 +135,9 @@ __device__ __forceinline__ bf16x8 operand(const bf16* tile, int mn0, int k0, int
   }
 }
 
-// Wave w = (wm, wn) = (w / 4, w % 4) owns outputs m0 + 128wm .. +127,
-// n0 + 64wn .. +63: acc.v[i][j][r] = C[m0 + 128wm + 32i + 8(r/4) + 4g + r%4][n0 + 64wn + 32j + c32].
+// Wave w = (wm, wn) = (w / NWN, w % NWN) owns outputs m0 + WTM wm .. + WTM - 1,
+// n0 + WTN wn .. + WTN - 1:
+// acc.v[i][j][r] = C[m0 + WTM wm + 32i + 8(r/4) + 4g + r%4][n0 + WTN wn + 32j + c32].
 struct Acc {
   f32x16 v[TI][TJ];
   __device__ __forceinline__ void zero() {
@@ -150,9 +157,9 @@ __device__ __forceinline__ void mma_stage(const bf16* As, const bf16* Bs, Acc& a
   for (int ks = 0; ks < BK / 16; ++ks) {
     bf16x8 a[TI], b[TJ];
 #pragma unroll
-    for (int i = 0; i < TI; ++i) a[i] = operand<AKC>(As, 128 * wm + 32 * i, 16 * ks, lane);
+    for (int i = 0; i < TI; ++i) a[i] = operand<AKC>(As, WTM * wm + 32 * i, 16 * ks, lane);
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) b[j] = operand<BKC>(Bs, 64 * wn + 32 * j, 16 * ks, lane);
+    for (int j = 0; j < TJ; ++j) b[j] = operand<BKC>(Bs, WTN * wn + 32 * j, 16 * ks, lane);
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -167,7 +174,7 @@ template <bool AKC, bool BKC>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int m0, int n0,
                                           bf16* As, bf16* Bs, Acc& acc, int tid) {
   const int w = tid >> 6, lane = tid & 63;
-  const int wm = w >> 2, wn = w & 3;
+  const int wm = w / NWN, wn = w % NWN;
   const int K = A.K;
   const int nk = (K + BK - 1) / BK;
   TileAddr<AKC> aa;
@@ -209,16 +216,28 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   }
 }
 
+// x^n, n = 2^log2n: unrolled squarings for a compile-time L2N > 0 (a runtime
+// loop inside the per-logit epilogue would cost a branch per logit).
+template <int L2N> __device__ __forceinline__ float pow_n(float x, int log2n) {
+  if (L2N > 0) {
+#pragma unroll
+    for (int i = 0; i < L2N; ++i) x = x * x;
+    return x;
+  }
+  return pow2n(x, log2n);
+}
+
 // alg_ce weight w = (x + sqrt(1+x^2))^n with x = min(z/c, clamp) (fused_head.py:98-100).
+template <int L2N>
 __device__ __forceinline__ float alg_weight(float z, float inv_c, float clamp, int log2n,
                                             float& r) {
   const float x = __builtin_fminf(z * inv_c, clamp);
-  return pow2n(rho_fast(x, r), log2n);
+  return pow_n<L2N>(rho_fast(x, r), log2n);
 }
 
 // Forward statistics. grid = (token blocks) x (vocabulary chunks).
 // partial[(chunk * N + token) * 2 + {0,1}] = (m, l) for ce, (-, l) for alg_ce.
-template <int KIND>
+template <int KIND, int L2N>
 __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
     const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
     float* __restrict__ zt, float* __restrict__ partial, int N, int d, int V, int log2n,
@@ -227,7 +246,7 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
   __shared__ __attribute__((aligned(16))) bf16 Bs[2 * kStageElems];
   __shared__ float red_m[2][BN], red_l[2][BN];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
-  const int wm = w >> 2, wn = w & 3;
+  const int wm = w / NWN, wn = w % NWN;
   const int n0 = blockIdx.x * BN;
   const int chunk = blockIdx.y;
   const int ntiles_v = (V + BM - 1) / BM;
@@ -239,25 +258,36 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
   float m_st[TJ], l_st[TJ];
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
-    tok[j] = n0 + 64 * wn + 32 * j + c32;
+    tok[j] = n0 + WTN * wn + 32 * j + c32;
     tgt[j] = tok[j] < N ? targets[tok[j]] : -1;
     m_st[j] = -1e30f;
     l_st[j] = 0.0f;
   }
-  Acc acc;
-  for (int t = t_begin; t < t_end; ++t) {
-    const int m0 = t * BM;
-    gemm_tile<true, true>(A, B, m0, n0, As, Bs, acc, tid);
+  // Statistic update of one vocabulary tile; FULL: every row of the tile is
+  // inside the vocabulary (all but the last tile), so no row mask is formed.
+  auto consume = [&](auto full_tag, int m0, const Acc& acc) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    const int mw = m0 + WTM * wm;
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
+      // The target logit: one lane of one 32-row block holds it.
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+        const int off = tgt[j] - (mw + 32 * i);
+        if (off >= 0 && off < 32 && ((off >> 2) & 1) == g) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (8 * (r >> 2) + (r & 3) == (off & ~4)) zt[tok[j]] = acc.v[i][j][r];
+        }
+      }
       float tile_max = -1e30f;
       if (KIND == ALGX_HEAD_CE) {
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int m = m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (m < V) tile_max = __builtin_fmaxf(tile_max, acc.v[i][j][r]);
+            const int m = mw + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (FULL || m < V) tile_max = __builtin_fmaxf(tile_max, acc.v[i][j][r]);
           }
       }
       const float m_new = __builtin_fmaxf(m_st[j], tile_max);
@@ -266,17 +296,16 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
       for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int m = m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+          const int m = mw + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
           const float z = acc.v[i][j][r];
-          if (m == tgt[j]) zt[tok[j]] = z;
           float wgt;
           if (KIND == ALGX_HEAD_CE) {
             wgt = __builtin_amdgcn_exp2f((z - m_new) * 1.4426950408889634f);
           } else {
             float rr;
-            wgt = alg_weight(z, inv_c, clamp, log2n, rr);
+            wgt = alg_weight<L2N>(z, inv_c, clamp, log2n, rr);
           }
-          lsum += m < V ? wgt : 0.0f;
+          lsum += (FULL || m < V) ? wgt : 0.0f;
         }
       if (KIND == ALGX_HEAD_CE) {
         l_st[j] = l_st[j] * __builtin_amdgcn_exp2f((m_st[j] - m_new) * 1.4426950408889634f) + lsum;
@@ -285,6 +314,15 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
         l_st[j] += lsum;
       }
     }
+  };
+  Acc acc;
+  for (int t = t_begin; t < t_end; ++t) {
+    const int m0 = t * BM;
+    gemm_tile<true, true>(A, B, m0, n0, As, Bs, acc, tid);
+    if (m0 + BM <= V)
+      consume(std::true_type{}, m0, acc);
+    else
+      consume(std::false_type{}, m0, acc);
   }
   // Merge the 4 partial states of each token: lane halves g, then waves wm.
 #pragma unroll
@@ -299,8 +337,8 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
       l_st[j] += lo;
     }
     if (g == 0) {
-      red_m[wm][64 * wn + 32 * j + c32] = m_st[j];
-      red_l[wm][64 * wn + 32 * j + c32] = l_st[j];
+      red_m[wm][WTN * wn + 32 * j + c32] = m_st[j];
+      red_l[wm][WTN * wn + 32 * j + c32] = l_st[j];
     }
   }
   __syncthreads();
@@ -349,7 +387,7 @@ __global__ __launch_bounds__(256) void head_stat_kernel(const float* __restrict_
 }
 
 // dz tile of a token chunk: dz[t][v] = bf16(f(z) * scale), 0 for padded v.
-template <int KIND>
+template <int KIND, int L2N>
 __global__ __launch_bounds__(kThreads) void head_dz_kernel(
     const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
     const float* __restrict__ stat, const float* __restrict__ scale, bf16* __restrict__ dz,
@@ -357,7 +395,7 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
   __shared__ __attribute__((aligned(16))) bf16 As[2 * kStageElems];
   __shared__ __attribute__((aligned(16))) bf16 Bs[2 * kStageElems];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
-  const int wm = w >> 2, wn = w & 3;
+  const int wm = w / NWN, wn = w % NWN;
   const int n0 = blockIdx.x * BN;   // token offset inside the chunk
   const int m0 = blockIdx.y * BM;   // vocabulary offset
   const Operand A{e, d, V, d};
@@ -365,37 +403,46 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
   Acc acc;
   gemm_tile<true, true>(A, B, m0, n0, As, Bs, acc, tid);
   const float sc = scale[0];
+  // FULL: every row of the tile is inside the vocabulary (all but the last
+  // vocabulary tile), so no row mask is formed.
+  auto emit = [&](auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
-  for (int j = 0; j < TJ; ++j) {
-    const int tl = n0 + 64 * wn + 32 * j + c32;
-    if (tl >= ntok) continue;
-    const int tgt = targets[tok0 + tl];
-    const float st = stat[tok0 + tl];
+    for (int j = 0; j < TJ; ++j) {
+      const int tl = n0 + WTN * wn + 32 * j + c32;
+      if (tl >= ntok) continue;
+      const int tgt = targets[tok0 + tl];
+      const float st = stat[tok0 + tl];
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int mb = m0 + 128 * wm + 32 * i + 8 * q4 + 4 * g;
-        bf16x4 out;
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int mb = m0 + WTM * wm + 32 * i + 8 * q4 + 4 * g;
+          bf16x4 out;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int m = mb + u;
-          const float z = acc.v[i][j][4 * q4 + u];
-          const float y = m == tgt ? 1.0f : 0.0f;
-          float g_z;
-          if (KIND == ALGX_HEAD_CE) {
-            g_z = __builtin_amdgcn_exp2f((z - st) * 1.4426950408889634f) - y;
-          } else {
-            const float x = __builtin_fminf(z * inv_c, clamp);
-            float r;
-            const float p = pow2n(rho_fast(x, r) * st, log2n);
-            g_z = (p - y) * r;
+          for (int u = 0; u < 4; ++u) {
+            const int m = mb + u;
+            const float z = acc.v[i][j][4 * q4 + u];
+            const float y = m == tgt ? 1.0f : 0.0f;
+            float g_z;
+            if (KIND == ALGX_HEAD_CE) {
+              g_z = __builtin_amdgcn_exp2f((z - st) * 1.4426950408889634f) - y;
+            } else {
+              const float x = __builtin_fminf(z * inv_c, clamp);
+              float r;
+              const float p = pow_n<L2N>(rho_fast(x, r) * st, log2n);
+              g_z = (p - y) * r;
+            }
+            out[u] = (bf16)((FULL || m < V) ? g_z * sc : 0.0f);
           }
-          out[u] = (bf16)(m < V ? g_z * sc : 0.0f);
+          *reinterpret_cast<bf16x4*>(dz + (int64_t)tl * ldz + mb) = out;
         }
-        *reinterpret_cast<bf16x4*>(dz + (int64_t)tl * ldz + mb) = out;
-      }
-  }
+    }
+  };
+  if (m0 + BM <= V)
+    emit(std::true_type{});
+  else
+    emit(std::false_type{});
 }
 
 // One GEMM of a grouped launch: C[m][n] (+)= sum_k A(m,k) B(n,k).
@@ -411,7 +458,7 @@ template <bool AKC, bool BKC, typename TOut, bool ACCUM>
 __device__ __forceinline__ void gemm_job(const GemmJob& jb, int tile, bf16* As, bf16* Bs,
                                          int tid) {
   const int w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
-  const int wm = w >> 2, wn = w & 3;
+  const int wm = w / NWN, wn = w % NWN;
   const int m0 = (tile / jb.tiles_n) * BM, n0 = (tile % jb.tiles_n) * BN;
   Acc acc;
   gemm_tile<AKC, BKC>(jb.A, jb.B, m0, n0, As, Bs, acc, tid);
@@ -420,11 +467,11 @@ __device__ __forceinline__ void gemm_job(const GemmJob& jb, int tile, bf16* As, 
   for (int i = 0; i < TI; ++i)
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
-      const int n = n0 + 64 * wn + 32 * j + c32;
+      const int n = n0 + WTN * wn + 32 * j + c32;
       if (n >= jb.N) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+        const int m = m0 + WTM * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
         if (m >= jb.M) continue;
         TOut* dst = C + (int64_t)m * jb.ldc + n;
         if (ACCUM)
@@ -478,6 +525,31 @@ int32_t check_head(const void* h, const void* E, const int32_t* targets, int N, 
   return 0;
 }
 
+typedef void (*HeadFwdFn)(const bf16*, const bf16*, const int32_t*, float*, float*, int, int,
+                          int, int, float, float);
+typedef void (*HeadDzFn)(const bf16*, const bf16*, const int32_t*, const float*, const float*,
+                         bf16*, int64_t, int, int, int, int, int, float, float);
+
+// Kernel instance for (kind, n): alg_ce with n = 8, 16 or 32 gets unrolled powers.
+HeadFwdFn pick_head_fwd(int kind, int log2n) {
+  if (kind == ALGX_HEAD_CE) return head_fwd_kernel<ALGX_HEAD_CE, 0>;
+  switch (log2n) {
+    case 3: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 3>;
+    case 4: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 4>;
+    case 5: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 5>;
+    default: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 0>;
+  }
+}
+HeadDzFn pick_head_dz(int kind, int log2n) {
+  if (kind == ALGX_HEAD_CE) return head_dz_kernel<ALGX_HEAD_CE, 0>;
+  switch (log2n) {
+    case 3: return head_dz_kernel<ALGX_HEAD_ALG_CE, 3>;
+    case 4: return head_dz_kernel<ALGX_HEAD_ALG_CE, 4>;
+    case 5: return head_dz_kernel<ALGX_HEAD_ALG_CE, 5>;
+    default: return head_dz_kernel<ALGX_HEAD_ALG_CE, 0>;
+  }
+}
+
 int nchunks_of(int V) {
   const int nt = (V + BM - 1) / BM;
   return (nt + kVocabChunkTiles - 1) / kVocabChunkTiles;
@@ -511,7 +583,7 @@ extern "C" int32_t algx_head_fwd(const void* h, const void* E, const int32_t* ta
   if (int32_t rc = fill_f32(zt, N, 0.0f, s)) return rc;
   {
     const Probe probe = probe_for(ALGX_PROBE_HEAD_FWD);
-    launch_k(probe, kind == ALGX_HEAD_CE ? head_fwd_kernel<ALGX_HEAD_CE> : head_fwd_kernel<ALGX_HEAD_ALG_CE>,
+    launch_k(probe, pick_head_fwd(kind, log2n),
              grid, dim3(kThreads), s, (const bf16*)h, (const bf16*)E, targets, zt, partial, N, d,
              V, log2n, inv_c, clamp);
   }
@@ -552,7 +624,7 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
     const int ntok = min(csize, N - tok0);
     dim3 gdz((ntok + BN - 1) / BN, (V + BM - 1) / BM);
     launch_k(probe_for(ALGX_PROBE_HEAD_DZ),
-             kind == ALGX_HEAD_CE ? head_dz_kernel<ALGX_HEAD_CE> : head_dz_kernel<ALGX_HEAD_ALG_CE>,
+             pick_head_dz(kind, log2n),
              gdz, dim3(kThreads), s, hb, eb, targets, stat, scale, dz, ldz, tok0, ntok, d, V, log2n,
              inv_c, clamp);
     if (int32_t rc = check_launch("head_dz")) return rc;
