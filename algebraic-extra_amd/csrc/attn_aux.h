@@ -42,8 +42,9 @@ int32_t launch_fwd_mfma(const void* q_s, const void* k, const void* v, const flo
                         hipStream_t s);
 // Pre-scale, guard and forward in one pass over q (MFMA shapes): the low
 // variant runs over the whole grid writing q_s and, guarded, one triple of
-// partial maxima per workgroup (fwd_fused_partials of them); the guard word
-// follows, then a high-variant launch that returns at once when in range.
+// partial maxima per workgroup (fwd_fused_partials of them); a second launch
+// reduces them to the guard word and, out of range only, runs the high
+// variant.
 int64_t fwd_fused_partials(int B, int H, int T);
 int32_t launch_fwd_fused(const void* q, const void* k, const void* v, const float* sink,
                          void* q_s, void* o, float* o_precise, float* stat, int32_t* guard,

@@ -29,10 +29,10 @@ __device__ __forceinline__ void fwd_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
     float* __restrict__ stat, int H, int T_, const KVariant& var, const FwdPrep& prep,
-    bf16 (*Ks)[FBN * KSTR], bf16 (*Vs)[FBN * VSTR], float (*red)[4]) {
-  const int nheads = gridDim.x / (T_ / FBM);
+    bf16 (*Ks)[FBN * KSTR], bf16 (*Vs)[FBN * VSTR], float (*red)[4], int bid, int nblocks) {
+  const int nheads = nblocks / (T_ / FBM);
   int bh, qb;
-  map_block(blockIdx.x, nheads, T_ / FBM, true, bh, qb);
+  map_block(bid, nheads, T_ / FBM, true, bh, qb);
   const int h = bh % H;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
   const int G = lane >> 4, j4 = (lane >> 2) & 3, m4 = lane & 3;
@@ -99,7 +99,7 @@ __device__ __forceinline__ void fwd_body(
       }
       __syncthreads();
       if (tid < 3)
-        prep.partial[(int64_t)blockIdx.x * 3 + tid] =
+        prep.partial[(int64_t)bid * 3 + tid] =
             __builtin_fmaxf(__builtin_fmaxf(red[tid][0], red[tid][1]),
                             __builtin_fmaxf(red[tid][2], red[tid][3]));
     }
@@ -324,9 +324,7 @@ __device__ __forceinline__ void fwd_body(
 }
 
 // The guard word (if any) picks the low or the high variant for the whole
-// grid, mirroring lax.cond(in_range, low, high). A launch with prep.skip set
-// is the high half of the fused call: it does nothing when that guard word
-// says in range.
+// grid, mirroring lax.cond(in_range, low, high).
 template <int LO, int HI>
 __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
@@ -336,13 +334,87 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   __shared__ __attribute__((aligned(16))) bf16 Ks[2][FBN * KSTR];
   __shared__ __attribute__((aligned(16))) bf16 Vs[2][FBN * VSTR];
   __shared__ float red[3][4];
-  if (prep.skip != nullptr && guard_in_range(prep.skip)) return;
   if (LO == HI || guard_in_range(guard))
-    fwd_body<LO & 3, (LO & 4) != 0, (LO & 8) != 0, (LO >> 4)>(q, k, v, sink, o, o_precise, stat,
-                                                              H, T_, lo, prep, Ks, Vs, red);
+    fwd_body<LO & 3, (LO & 4) != 0, (LO & 8) != 0, (LO >> 4)>(
+        q, k, v, sink, o, o_precise, stat, H, T_, lo, prep, Ks, Vs, red, blockIdx.x, gridDim.x);
   else
-    fwd_body<HI & 3, (HI & 4) != 0, (HI & 8) != 0, (HI >> 4)>(q, k, v, sink, o, o_precise, stat,
-                                                              H, T_, hi, prep, Ks, Vs, red);
+    fwd_body<HI & 3, (HI & 4) != 0, (HI & 8) != 0, (HI >> 4)>(
+        q, k, v, sink, o, o_precise, stat, H, T_, hi, prep, Ks, Vs, red, blockIdx.x, gridDim.x);
+}
+
+// The guard's closing step and the high half of lax.cond in one launch.
+// Every workgroup reduces the low launch's partial maxima to the same
+// decision (flash.py:843-849: in range iff max|q_s|^2 max|k|^2 <= (b/1.01)^2,
+// max|sink| <= b/1.01 and max|v| <= vmax); workgroup 0 stores the guard word
+// for the backward. In range, that is all; otherwise the grid walks every
+// (head, query tile) with the high variant.
+struct GuardIn {
+  const float* partial;
+  int nparts;
+  float bound_sq, bound_s, vmax;
+  int32_t* guard;
+};
+
+template <int HI>
+__global__ __launch_bounds__(256, 2) void fwd_fallback_kernel(
+    const bf16* __restrict__ q_s, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
+    float* __restrict__ stat, int H, int T_, KVariant hi, GuardIn gin, int ntiles) {
+  __shared__ __attribute__((aligned(16))) bf16 Ks[2][FBN * KSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[2][FBN * VSTR];
+  __shared__ float red[3][4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  float mx[3] = {0.0f, 0.0f, 0.0f};
+  for (int b = tid; b < gin.nparts; b += 256)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) mx[j] = __builtin_fmaxf(mx[j], gin.partial[(int64_t)b * 3 + j]);
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) mx[j] = __builtin_fmaxf(mx[j], __shfl_xor(mx[j], m, 64));
+  if (lane == 0)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) red[j][w] = mx[j];
+  __syncthreads();
+  float tot[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+    tot[j] = __builtin_fmaxf(__builtin_fmaxf(red[j][0], red[j][1]), __builtin_fmaxf(red[j][2], red[j][3]));
+  float ms = 0.0f;
+  if (sink != nullptr)
+    for (int h = 0; h < H; ++h) {
+      const float a = __builtin_fabsf(sink[h]);
+      ms = __builtin_fmaxf(ms, a != a ? __builtin_inff() : a);
+    }
+  bool ok = tot[0] * tot[1] <= gin.bound_sq && tot[2] <= gin.vmax;
+  if (sink != nullptr) ok = ok && ms <= gin.bound_s;
+  if (blockIdx.x == 0 && tid == 0) {
+    gin.guard[0] = ok ? 1 : 0;
+    float* f = reinterpret_cast<float*>(gin.guard);
+    f[1] = tot[0];
+    f[2] = tot[1];
+    f[3] = tot[2];
+    f[4] = ms;
+  }
+  if (ok) return;
+  for (int b = blockIdx.x; b < ntiles; b += gridDim.x) {
+    __syncthreads();  // LDS of the previous tile is no longer read
+    fwd_body<HI & 3, (HI & 4) != 0, (HI & 8) != 0, (HI >> 4)>(
+        q_s, k, v, sink, o, o_precise, stat, H, T_, hi, FwdPrep{}, Ks, Vs, red, b, ntiles);
+  }
+}
+
+typedef void (*FallbackFn)(const bf16*, const bf16*, const bf16*, const float*, bf16*, float*,
+                           float*, int, int, KVariant, GuardIn, int);
+
+// The high variants a guarded call pairs with (shifted, exact rho), as for
+// the guarded two-variant kernels.
+FallbackFn pick_fallback(int ch) {
+  if (ch == cfg_of(MODE_SHIFT, false, false, 3)) return fwd_fallback_kernel<cfg_of(MODE_SHIFT, false, false, 3)>;
+  if (ch == cfg_of(MODE_SHIFT, false, false, 4)) return fwd_fallback_kernel<cfg_of(MODE_SHIFT, false, false, 4)>;
+  if (ch == cfg_of(MODE_SHIFT, false, false, 5)) return fwd_fallback_kernel<cfg_of(MODE_SHIFT, false, false, 5)>;
+  if (ch == cfg_of(MODE_SHIFT, false, false, 0)) return fwd_fallback_kernel<cfg_of(MODE_SHIFT, false, false, 0)>;
+  return nullptr;
 }
 
 typedef void (*FwdFn)(const bf16*, const bf16*, const bf16*, const float*, bf16*, float*, float*,
@@ -385,19 +457,19 @@ int32_t launch_fwd_fused(const void* q, const void* k, const void* v, const floa
   // overwritten by the high launch below.
   FwdFn fn = pick_fwd(cfg_for(lo), cfg_for(lo));
   if (fn == nullptr) return fail("attn_forward: no MFMA kernel for the low variant");
-  FwdPrep pre{(bf16*)q_s, q_scale, guard != nullptr ? partial : nullptr, nullptr};
+  FwdPrep pre{(bf16*)q_s, q_scale, guard != nullptr ? partial : nullptr};
   launch_k(probe_for(ALGX_PROBE_ATTN_FWD), fn, dim3(grid), dim3(256), s, (const bf16*)q,
            (const bf16*)k, (const bf16*)v, sink, (bf16*)o, o_precise, stat, H, T, lo, lo,
            (const int32_t*)nullptr, pre);
   if (int32_t rc = check_launch("attn_forward_low")) return rc;
   if (guard == nullptr) return 0;
-  if (int32_t rc = launch_guard_finish(partial, grid, sink, H, bound, vmax, guard, s)) return rc;
-  FwdFn fh = pick_fwd(cfg_for(hi), cfg_for(hi));
+  FallbackFn fh = pick_fallback(cfg_for(hi));
   if (fh == nullptr) return fail("attn_forward: no MFMA kernel for the high variant");
-  FwdPrep skip{nullptr, 0.0f, nullptr, guard};
-  launch_k(Probe{}, fh, dim3(grid), dim3(256), s, (const bf16*)q_s, (const bf16*)k,
-           (const bf16*)v, sink, (bf16*)o, o_precise, stat, H, T, hi, hi,
-           (const int32_t*)nullptr, skip);
+  const double b101 = (double)bound / 1.01;
+  const GuardIn gin{partial, grid, (float)(b101 * b101), (float)b101, vmax, guard};
+  const int fgrid = grid < 512 ? grid : 512;  // two workgroups per CU
+  launch_k(Probe{}, fh, dim3(fgrid), dim3(256), s, (const bf16*)q_s, (const bf16*)k,
+           (const bf16*)v, sink, (bf16*)o, o_precise, stat, H, T, hi, gin, grid);
   return check_launch("attn_forward_high");
 }
 

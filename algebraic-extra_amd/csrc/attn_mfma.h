@@ -16,13 +16,11 @@ enum { MODE_SOFTMAX = 0, MODE_NOSHIFT = 1, MODE_SHIFT = 2 };
 
 // Extra work of a forward launch: q_s != null -> `q` is the raw query and the
 // kernel writes q_s = cast(q * q_scale); partial != null -> it also writes the
-// range guard's three partial maxima per workgroup; skip != null -> the launch
-// does nothing when that guard word says in range.
+// range guard's three partial maxima per workgroup.
 struct FwdPrep {
   bf16* q_s = nullptr;
   float q_scale = 1.0f;
   float* partial = nullptr;
-  const int32_t* skip = nullptr;
 };
 
 // s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt left unconstrained

@@ -115,9 +115,10 @@ int32_t algx_attn_fwd(const void* q_s, const void* k, const void* v, const float
  * For bf16, D = 64, T % 128 == 0 the forward kernel reads the raw q itself,
  * writes q_s (for the backward) and, with a guard buffer, one triple of
  * partial guard maxima per workgroup into `workspace`
- * (algx_attn_forward_workspace_bytes; may be NULL when guard is NULL); the
- * guard word follows, and a high-variant launch that does nothing when the
- * word says in range completes lax.cond. Other shapes run the two calls. */
+ * (algx_attn_forward_workspace_bytes; may be NULL when guard is NULL). A
+ * second launch reduces them to the guard word and, only when out of range,
+ * recomputes the forward with `high`, completing lax.cond. Other shapes run
+ * the two calls. */
 int64_t algx_attn_forward_workspace_bytes(int32_t B, int32_t H, int32_t T, int32_t D);
 int32_t algx_attn_forward(const void* q, const void* k, const void* v, const float* sink,
                           void* q_s, void* o, float* o_precise, float* stat, int32_t* guard,
