@@ -153,10 +153,17 @@ def bench_head(steps, warmup, dev, N=16384, d=768, V=50304, kind="alg_ce", n=8, 
         torch.autograd.grad(obj, (h, E))
 
     dt = time_steps(step, steps, warmup)
+    # Kernel split (HIP events recorded with each kernel's dispatch): the
+    # forward statistics, the dz recompute and the grouped dh + dE GEMMs.
+    split = {}
+    for name in ("head_fwd", "head_dz", "head_de"):
+        pr = Probe(name, steps)
+        time_steps(step, steps, 1, pr, settle_s=0.0)
+        split[{"head_fwd": "fwd_ms", "head_dz": "dz_ms", "head_de": "dh_dE_ms"}[name]] = pr.mean_ms()
     flops = 3 * 2 * N * d * V
     return {"workload": f"N={N},d={d},V={V},{kind} n={n} c={c}", "ms_per_step": dt * 1e3,
             "tokens_per_s": N / dt, "tflops": flops / dt / 1e12,
-            "frac": flops / dt / 1e12 / PEAK_BF16_TFLOPS}
+            "frac": flops / dt / 1e12 / PEAK_BF16_TFLOPS, **split}
 
 
 def bench_qknorm(steps, warmup, dev):
@@ -220,6 +227,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true", help="skip the head/QK-norm lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--head-only", action="store_true",
+                    help="time only the fused head (configs[2]) and print its line (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 256 MiB device copy (scale reference for the "
                          "FETCH_SIZE/WRITE_SIZE counters of a rocprofv3 --pmc run)")
@@ -237,6 +246,11 @@ def main():
     _lib.load()
     dev = "cuda:0"
     B, H, T, D = 8, 12, 2048, 64
+    if args.head_only:
+        print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
+                          for k, v in bench_head(args.steps, args.warmup, dev).items()}),
+              flush=True)
+        return
     if args.calibrate_copy:
         src = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
         dst = torch.empty_like(src)
