@@ -14,7 +14,8 @@ BF16, F32 = 0, 1
 SOFTMAX, ASINH = 0, 1
 HEAD_CE, HEAD_ALG_CE = 0, 1
 PROBE = {"none": 0, "attn_fwd": 1, "attn_bwd": 2, "head_fwd": 3, "head_dz": 4, "head_dh": 5,
-         "head_de": 6, "qknorm_fwd": 7, "qknorm_bwd": 8}
+         "head_de": 6, "qknorm_fwd": 7, "qknorm_bwd": 8, "rms_norm_fwd": 9, "rms_norm_bwd": 10,
+         "alu_fwd": 11, "alu_bwd": 12}
 
 _i32, _i64, _f32, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -54,6 +55,13 @@ SIGNATURES = {
     "algx_head_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "algx_head_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32,
                              _f32, _f32, _i32, _p]),
+    "algx_rms_norm_fwd": (_i32, [_p, _p, _p, _i64, _i32, _i32, _f32, _p]),
+    "algx_rms_norm_bwd_workspace_bytes": (_i64, [_i64, _i32, _i32]),
+    "algx_rms_norm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _f32, _p]),
+    "algx_alu_fwd": (_i32, [_p, _p, _i64, _i32, _f32, _p]),
+    "algx_alu_bwd": (_i32, [_p, _p, _p, _i64, _i32, _f32, _p]),
+    "algx_alu_glu_fwd": (_i32, [_p, _p, _p, _i64, _i32, _f32, _p]),
+    "algx_alu_glu_bwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _f32, _p]),
 }
 
 _lib = None

@@ -26,8 +26,6 @@ int32_t check_launch(const char* what);
 // Fills n floats on stream s with a kernel (no memset node).
 int32_t fill_f32(float* p, int64_t n, float value, hipStream_t s);
 
-// Records the registered probe events around one kernel launch (see
-// algx_set_probe): construct just before the launch, destroy just after.
 // HIP events armed by algx_set_probe for one kernel. A probed launch hands
 // them to hipExtLaunchKernel, which records them as part of the kernel's own
 // dispatch: timing inserts no extra packets (and no cache fences) between

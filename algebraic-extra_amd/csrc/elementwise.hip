@@ -1,0 +1,490 @@
+// The model's elementwise algebraic ops around the attention path
+// (algebraic.py:76-117): RMS normalisation of d_model-wide rows with an
+// optional float32 gain (rms_norm; no gain is the parameter-free AVN) and the
+// algebraic linear unit alu(x) = x/2 (1 + bx / sqrt(1 + b^2 x^2)) with its
+// custom VJP, plus the model's gated product gate * alu(up) fused into one
+// pass (model.py:186-191).
+//
+// All of it is HBM-bound: one pass over the operands with 16-byte accesses.
+// A norm row belongs to one wave (its D/8 bf16 or D/4 f32 chunks spread over
+// the 64 lanes), so the row sums are wave reductions. dgain is reduced per
+// workgroup into a workspace row and finished per column in a fixed order
+// (deterministic).
+#include <initializer_list>
+
+#include "common.h"
+
+namespace algx {
+
+namespace {
+
+constexpr int kFwdThreads = 256;
+constexpr int kBwdThreads = 1024;
+constexpr int kBwdWaves = kBwdThreads / 64;
+constexpr int kMaxD = 1024;
+constexpr int kMaxBwdBlocks = 512;
+constexpr int kEltThreads = 256;
+
+template <typename T> struct Vec;
+template <> struct Vec<bf16> { typedef bf16x8 type; static constexpr int n = 8; };
+template <> struct Vec<float> { typedef f32x4 type; static constexpr int n = 4; };
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// Gain values of this lane's chunks (1 where there is no gain).
+template <int CPL, int EPL>
+__device__ __forceinline__ void load_gain(const float* gain, int lane, int nch,
+                                          float (&g)[CPL][EPL]) {
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = lane + 64 * c;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e)
+      g[c][e] = (gain != nullptr && ch < nch) ? gain[ch * EPL + e] : 1.0f;
+  }
+}
+
+// y = cast((x * tau) * gain), tau = rsqrt(mean(x^2) + eps) (algebraic.py:76-83).
+// One row per wave; CPL = 16-byte chunks per lane.
+template <typename T, int CPL>
+__global__ __launch_bounds__(kFwdThreads) void rmsnorm_fwd_kernel(const T* __restrict__ x,
+                                                                  const float* __restrict__ gain,
+                                                                  T* __restrict__ y, int64_t rows,
+                                                                  int D, float eps) {
+  typedef typename Vec<T>::type VT;
+  constexpr int EPL = Vec<T>::n;
+  const int lane = threadIdx.x & 63;
+  const int nch = D / EPL;
+  float g[CPL][EPL];
+  load_gain<CPL, EPL>(gain, lane, nch, g);
+  const int64_t stride = (int64_t)gridDim.x * (kFwdThreads / 64);
+  const float inv_d = 1.0f / (float)D;
+  for (int64_t row = (int64_t)blockIdx.x * (kFwdThreads / 64) + (threadIdx.x >> 6); row < rows;
+       row += stride) {
+    const T* xr = x + row * D;
+    VT in[CPL];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = lane + 64 * c;
+      if (ch < nch) {
+        in[c] = *reinterpret_cast<const VT*>(xr + ch * EPL);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          const float f = to_f(in[c][e]);
+          ss = __builtin_fmaf(f, f, ss);
+        }
+      }
+    }
+    const float tau = rsq(wave_sum(ss) * inv_d + eps);
+    T* yr = y + row * D;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = lane + 64 * c;
+      if (ch < nch) {
+        VT out;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) out[e] = from_f<T>((to_f(in[c][e]) * tau) * g[c][e]);
+        *reinterpret_cast<VT*>(yr + ch * EPL) = out;
+      }
+    }
+  }
+}
+
+// Input VJP of rms_norm (autodiff of algebraic.py:76-83 through mean/rsqrt):
+//   dx = tau * gain * dy - x * tau^3 * sum(dy * gain * x) / D
+// and, given `partial` ([gridDim.x][D] float32), each workgroup's share of
+//   dgain = sum_rows dy * x * tau.
+template <typename T, int CPL>
+__global__ __launch_bounds__(kBwdThreads) void rmsnorm_bwd_kernel(
+    const T* __restrict__ x, const float* __restrict__ gain, const T* __restrict__ dy,
+    T* __restrict__ dx, float* __restrict__ partial, int64_t rows, int D, float eps) {
+  typedef typename Vec<T>::type VT;
+  constexpr int EPL = Vec<T>::n;
+  __shared__ float red[kBwdWaves][kMaxD];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nch = D / EPL;
+  float g[CPL][EPL], dg[CPL][EPL];
+  load_gain<CPL, EPL>(gain, lane, nch, g);
+#pragma unroll
+  for (int c = 0; c < CPL; ++c)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) dg[c][e] = 0.0f;
+  const int64_t stride = (int64_t)gridDim.x * kBwdWaves;
+  const float inv_d = 1.0f / (float)D;
+  for (int64_t row = (int64_t)blockIdx.x * kBwdWaves + w; row < rows; row += stride) {
+    VT xi[CPL], gi[CPL];
+    float ss = 0.0f, dot = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = lane + 64 * c;
+      if (ch < nch) {
+        xi[c] = *reinterpret_cast<const VT*>(x + row * D + ch * EPL);
+        gi[c] = *reinterpret_cast<const VT*>(dy + row * D + ch * EPL);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          const float xf = to_f(xi[c][e]);
+          ss = __builtin_fmaf(xf, xf, ss);
+          dot = __builtin_fmaf(to_f(gi[c][e]) * g[c][e], xf, dot);
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    dot = wave_sum(dot);
+    const float tau = rsq(ss * inv_d + eps);
+    const float cfac = tau * tau * tau * dot * inv_d;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = lane + 64 * c;
+      if (ch < nch) {
+        VT out;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          const float xf = to_f(xi[c][e]), df = to_f(gi[c][e]);
+          out[e] = from_f<T>(tau * g[c][e] * df - cfac * xf);
+          dg[c][e] = __builtin_fmaf(df, xf * tau, dg[c][e]);
+        }
+        *reinterpret_cast<VT*>(dx + row * D + ch * EPL) = out;
+      }
+    }
+  }
+  if (partial == nullptr) return;
+  // Workgroup share of dgain: the waves' column sums added in wave order.
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = lane + 64 * c;
+    if (ch < nch)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) red[w][ch * EPL + e] = dg[c][e];
+  }
+  __syncthreads();
+  for (int col = threadIdx.x; col < D; col += kBwdThreads) {
+    float s = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < kBwdWaves; ++ww) s += red[ww][col];
+    partial[(int64_t)blockIdx.x * D + col] = s;
+  }
+}
+
+// dgain[col] = sum of the workgroup partials: 64 columns per workgroup, four
+// interleaved slices of the partial rows per column, combined in slice order.
+__global__ __launch_bounds__(256) void rmsnorm_gain_finish(const float* __restrict__ partial,
+                                                           int nparts, int D,
+                                                           float* __restrict__ dgain) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
+  float s = 0.0f;
+  if (col < D)
+    for (int b = slice; b < nparts; b += 4) s += partial[(int64_t)b * D + col];
+  red[slice][lane] = s;
+  __syncthreads();
+  if (slice == 0 && col < D) dgain[col] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+}
+
+// alu in float32 (algebraic.py:86-93): u = bz r, r = rsqrt(1 + (bz)^2),
+// alu = z/2 (1 + u) with 1 + u taken as r^2 / (1 - u) for bz < 0 so the
+// negative tail keeps its relative precision.
+__device__ __forceinline__ float alu_parts(float z, float beta, float& u, float& r) {
+  const float bz = beta * z;
+  r = rsq(__builtin_fmaf(bz, bz, 1.0f));
+  u = bz * r;
+  const float one_plus_u =
+      bz < 0.0f ? (r * r) * __builtin_amdgcn_rcpf(1.0f - u) : 1.0f + u;
+  return 0.5f * z * one_plus_u;
+}
+// d alu / dz = (1 + u)/2 + u r^2 / 2 (algebraic.py:109-111), with its one
+// fused multiply-add written out: hipcc contracts a * b + c wherever it finds
+// one, and which products it finds depends on what the caller shares with
+// alu_parts, so an implicit form rounds differently in the fused and the plain
+// backward kernels. (1 + u)/2 = 1/2 + u/2 exactly.
+__device__ __forceinline__ float alu_deriv(float u, float r) {
+  const float h = 0.5f * u;
+  return __builtin_fmaf(h, r * r, 0.5f + h);
+}
+
+// GLU = 0: y = cast(alu(a)).
+// GLU = 1: y = cast(b * cast(alu(a))), a = up, b = gate (model.py:186-191).
+template <typename T, int GLU>
+__global__ __launch_bounds__(kEltThreads) void alu_fwd_kernel(const T* __restrict__ a,
+                                                              const T* __restrict__ b,
+                                                              T* __restrict__ y, int64_t n,
+                                                              float beta) {
+  typedef typename Vec<T>::type VT;
+  constexpr int EPL = Vec<T>::n;
+  const int64_t nvec = n / EPL;
+  for (int64_t i = (int64_t)blockIdx.x * kEltThreads + threadIdx.x; i < nvec;
+       i += (int64_t)gridDim.x * kEltThreads) {
+    const VT av = reinterpret_cast<const VT*>(a)[i];
+    VT bv;
+    if (GLU) bv = reinterpret_cast<const VT*>(b)[i];
+    VT out;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float u, r;
+      const float act = round_to<T>(alu_parts(to_f(av[e]), beta, u, r));
+      out[e] = from_f<T>(GLU ? to_f(bv[e]) * act : act);
+    }
+    reinterpret_cast<VT*>(y)[i] = out;
+  }
+  // n % EPL trailing elements, one per thread of the first workgroup.
+  const int64_t t = nvec * EPL + threadIdx.x;
+  if (blockIdx.x == 0 && t < n) {
+    float u, r;
+    const float act = round_to<T>(alu_parts(to_f(a[t]), beta, u, r));
+    y[t] = from_f<T>(GLU ? to_f(b[t]) * act : act);
+  }
+}
+
+// GLU = 0: da = cast(dy * alu'(a)) (algebraic.py:108-112).
+// GLU = 1, out = b * act with act = cast(alu(a)):
+//   db = cast(dy * act), da = cast(cast(dy * b) * alu'(a)).
+template <typename T, int GLU>
+__global__ __launch_bounds__(kEltThreads) void alu_bwd_kernel(const T* __restrict__ a,
+                                                              const T* __restrict__ b,
+                                                              const T* __restrict__ dy,
+                                                              T* __restrict__ da,
+                                                              T* __restrict__ db, int64_t n,
+                                                              float beta) {
+  typedef typename Vec<T>::type VT;
+  constexpr int EPL = Vec<T>::n;
+  const int64_t nvec = n / EPL;
+  for (int64_t i = (int64_t)blockIdx.x * kEltThreads + threadIdx.x; i < nvec;
+       i += (int64_t)gridDim.x * kEltThreads) {
+    const VT av = reinterpret_cast<const VT*>(a)[i];
+    const VT gv = reinterpret_cast<const VT*>(dy)[i];
+    VT bv;
+    if (GLU) bv = reinterpret_cast<const VT*>(b)[i];
+    VT oa, ob;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float u, r;
+      const float g = to_f(gv[e]);
+      if (GLU) {
+        const float act = round_to<T>(alu_parts(to_f(av[e]), beta, u, r));
+        const float gact = round_to<T>(g * to_f(bv[e]));
+        oa[e] = from_f<T>(gact * alu_deriv(u, r));
+        ob[e] = from_f<T>(g * act);
+      } else {
+        const float bz = beta * to_f(av[e]);
+        r = rsq(__builtin_fmaf(bz, bz, 1.0f));
+        u = bz * r;
+        oa[e] = from_f<T>(g * alu_deriv(u, r));
+      }
+    }
+    reinterpret_cast<VT*>(da)[i] = oa;
+    if (GLU) reinterpret_cast<VT*>(db)[i] = ob;
+  }
+  const int64_t t = nvec * EPL + threadIdx.x;
+  if (blockIdx.x == 0 && t < n) {
+    float u, r;
+    const float act = round_to<T>(alu_parts(to_f(a[t]), beta, u, r));
+    const float g = to_f(dy[t]);
+    if (GLU) {
+      da[t] = from_f<T>(round_to<T>(g * to_f(b[t])) * alu_deriv(u, r));
+      db[t] = from_f<T>(g * act);
+    } else {
+      da[t] = from_f<T>(g * alu_deriv(u, r));
+    }
+  }
+}
+
+int fwd_blocks(int64_t rows) {
+  const int64_t per = kFwdThreads / 64;
+  int64_t nb = (rows + per - 1) / per;
+  return (int)(nb > 8192 ? 8192 : nb);
+}
+
+int bwd_blocks(int64_t rows) {
+  int64_t nb = (rows + kBwdWaves - 1) / kBwdWaves;
+  return (int)(nb > kMaxBwdBlocks ? kMaxBwdBlocks : nb);
+}
+
+int elt_blocks(int64_t nvec) {
+  int64_t nb = (nvec + kEltThreads - 1) / kEltThreads;
+  return (int)(nb > 8192 ? 8192 : nb);
+}
+
+int epl_of(int dtype) { return dtype == ALGX_BF16 ? 8 : 4; }
+
+int32_t check_norm(const void* x, int64_t rows, int32_t D, int32_t dtype, float eps) {
+  if (dtype != ALGX_BF16 && dtype != ALGX_F32) return fail("rms_norm: dtype must be bf16 or f32");
+  if (rows < 0) return fail("rms_norm: negative row count");
+  if (D <= 0 || D > kMaxD || D % epl_of(dtype))
+    return fail("rms_norm: D must be a multiple of 8 (bf16) or 4 (f32), at most 1024");
+  if (!(eps > 0.0f)) return fail("rms_norm: eps must be positive");
+  if (rows > 0 && x == nullptr) return fail("rms_norm: null input");
+  return 0;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int32_t check_alu(const void* a, int64_t n, int32_t dtype) {
+  if (dtype != ALGX_BF16 && dtype != ALGX_F32) return fail("alu: dtype must be bf16 or f32");
+  if (n < 0) return fail("alu: negative element count");
+  if (n > 0 && a == nullptr) return fail("alu: null input");
+  return 0;
+}
+
+// The 16-byte vector accesses need 16-byte aligned operands.
+int32_t check_aligned(std::initializer_list<const void*> ps, const char* what) {
+  for (const void* p : ps)
+    if (!aligned16(p)) return fail(std::string(what) + ": operands must be 16-byte aligned");
+  return 0;
+}
+
+template <typename T, int CPL>
+void launch_norm_fwd(const void* x, const float* gain, void* y, int64_t rows, int D, float eps,
+                     hipStream_t s) {
+  launch_k(probe_for(ALGX_PROBE_RMSNORM_FWD), rmsnorm_fwd_kernel<T, CPL>, dim3(fwd_blocks(rows)),
+           dim3(kFwdThreads), s, (const T*)x, gain, (T*)y, rows, D, eps);
+}
+
+template <typename T, int CPL>
+void launch_norm_bwd(const void* x, const float* gain, const void* dy, void* dx, float* partial,
+                     int64_t rows, int D, float eps, hipStream_t s) {
+  launch_k(probe_for(ALGX_PROBE_RMSNORM_BWD), rmsnorm_bwd_kernel<T, CPL>, dim3(bwd_blocks(rows)),
+           dim3(kBwdThreads), s, (const T*)x, gain, (const T*)dy, (T*)dx, partial, rows, D, eps);
+}
+
+}  // namespace
+}  // namespace algx
+
+using namespace algx;
+
+extern "C" int32_t algx_rms_norm_fwd(const void* x, const float* gain, void* y, int64_t rows,
+                                     int32_t D, int32_t dtype, float eps, void* stream) {
+  if (int32_t rc = check_norm(x, rows, D, dtype, eps)) return rc;
+  if (rows == 0) return 0;
+  if (y == nullptr) return fail("rms_norm: null output");
+  if (int32_t rc = check_aligned({x, y}, "rms_norm")) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  // Chunks per lane: ceil(D / (16-byte elements) / 64).
+  const int cpl = (D / epl_of(dtype) + 63) / 64;
+  if (dtype == ALGX_BF16) {
+    if (cpl == 1) launch_norm_fwd<bf16, 1>(x, gain, y, rows, D, eps, s);
+    else launch_norm_fwd<bf16, 2>(x, gain, y, rows, D, eps, s);
+  } else {
+    if (cpl == 1) launch_norm_fwd<float, 1>(x, gain, y, rows, D, eps, s);
+    else if (cpl == 2) launch_norm_fwd<float, 2>(x, gain, y, rows, D, eps, s);
+    else if (cpl == 3) launch_norm_fwd<float, 3>(x, gain, y, rows, D, eps, s);
+    else launch_norm_fwd<float, 4>(x, gain, y, rows, D, eps, s);
+  }
+  return check_launch("rms_norm_fwd");
+}
+
+extern "C" int64_t algx_rms_norm_bwd_workspace_bytes(int64_t rows, int32_t D, int32_t dtype) {
+  (void)dtype;
+  if (rows <= 0 || D <= 0) return 0;
+  return (int64_t)bwd_blocks(rows) * D * (int64_t)sizeof(float);
+}
+
+extern "C" int32_t algx_rms_norm_bwd(const void* x, const float* gain, const void* dy, void* dx,
+                                     float* dgain, void* workspace, int64_t rows, int32_t D,
+                                     int32_t dtype, float eps, void* stream) {
+  if (int32_t rc = check_norm(x, rows, D, dtype, eps)) return rc;
+  if ((gain == nullptr) != (dgain == nullptr))
+    return fail("rms_norm: dgain is required exactly when gain is given");
+  hipStream_t s = (hipStream_t)stream;
+  if (rows == 0) return dgain != nullptr ? fill_f32(dgain, D, 0.0f, s) : 0;
+  if (dy == nullptr || dx == nullptr) return fail("rms_norm: null dy/dx");
+  if (gain != nullptr && workspace == nullptr) return fail("rms_norm: null workspace");
+  if (int32_t rc = check_aligned({x, dy, dx}, "rms_norm")) return rc;
+  float* partial = gain != nullptr ? (float*)workspace : nullptr;
+  const int cpl = (D / epl_of(dtype) + 63) / 64;
+  if (dtype == ALGX_BF16) {
+    if (cpl == 1) launch_norm_bwd<bf16, 1>(x, gain, dy, dx, partial, rows, D, eps, s);
+    else launch_norm_bwd<bf16, 2>(x, gain, dy, dx, partial, rows, D, eps, s);
+  } else {
+    if (cpl == 1) launch_norm_bwd<float, 1>(x, gain, dy, dx, partial, rows, D, eps, s);
+    else if (cpl == 2) launch_norm_bwd<float, 2>(x, gain, dy, dx, partial, rows, D, eps, s);
+    else if (cpl == 3) launch_norm_bwd<float, 3>(x, gain, dy, dx, partial, rows, D, eps, s);
+    else launch_norm_bwd<float, 4>(x, gain, dy, dx, partial, rows, D, eps, s);
+  }
+  if (int32_t rc = check_launch("rms_norm_bwd")) return rc;
+  if (gain == nullptr) return 0;
+  rmsnorm_gain_finish<<<(D + 63) / 64, 256, 0, s>>>(partial, bwd_blocks(rows), D, dgain);
+  return check_launch("rms_norm_gain_finish");
+}
+
+namespace {
+
+template <typename T>
+int32_t alu_fwd_any(const void* up, const void* gate, void* y, int64_t n, float beta,
+                    hipStream_t s) {
+  const int64_t nvec = (n + Vec<T>::n - 1) / Vec<T>::n;
+  const Probe probe = probe_for(ALGX_PROBE_ALU_FWD);
+  if (gate == nullptr)
+    launch_k(probe, alu_fwd_kernel<T, 0>, dim3(elt_blocks(nvec)), dim3(kEltThreads), s,
+             (const T*)up, (const T*)nullptr, (T*)y, n, beta);
+  else
+    launch_k(probe, alu_fwd_kernel<T, 1>, dim3(elt_blocks(nvec)), dim3(kEltThreads), s,
+             (const T*)up, (const T*)gate, (T*)y, n, beta);
+  return check_launch("alu_fwd");
+}
+
+template <typename T>
+int32_t alu_bwd_any(const void* up, const void* gate, const void* dy, void* dup, void* dgate,
+                    int64_t n, float beta, hipStream_t s) {
+  const int64_t nvec = (n + Vec<T>::n - 1) / Vec<T>::n;
+  const Probe probe = probe_for(ALGX_PROBE_ALU_BWD);
+  if (gate == nullptr)
+    launch_k(probe, alu_bwd_kernel<T, 0>, dim3(elt_blocks(nvec)), dim3(kEltThreads), s,
+             (const T*)up, (const T*)nullptr, (const T*)dy, (T*)dup, (T*)nullptr, n, beta);
+  else
+    launch_k(probe, alu_bwd_kernel<T, 1>, dim3(elt_blocks(nvec)), dim3(kEltThreads), s,
+             (const T*)up, (const T*)gate, (const T*)dy, (T*)dup, (T*)dgate, n, beta);
+  return check_launch("alu_bwd");
+}
+
+}  // namespace
+
+extern "C" int32_t algx_alu_fwd(const void* x, void* y, int64_t n, int32_t dtype, float beta,
+                                void* stream) {
+  if (int32_t rc = check_alu(x, n, dtype)) return rc;
+  if (n == 0) return 0;
+  if (y == nullptr) return fail("alu: null output");
+  if (int32_t rc = check_aligned({x, y}, "alu")) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  return dtype == ALGX_BF16 ? alu_fwd_any<bf16>(x, nullptr, y, n, beta, s)
+                            : alu_fwd_any<float>(x, nullptr, y, n, beta, s);
+}
+
+extern "C" int32_t algx_alu_bwd(const void* x, const void* dy, void* dx, int64_t n, int32_t dtype,
+                                float beta, void* stream) {
+  if (int32_t rc = check_alu(x, n, dtype)) return rc;
+  if (n == 0) return 0;
+  if (dy == nullptr || dx == nullptr) return fail("alu: null dy/dx");
+  if (int32_t rc = check_aligned({x, dy, dx}, "alu")) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  return dtype == ALGX_BF16 ? alu_bwd_any<bf16>(x, nullptr, dy, dx, nullptr, n, beta, s)
+                            : alu_bwd_any<float>(x, nullptr, dy, dx, nullptr, n, beta, s);
+}
+
+extern "C" int32_t algx_alu_glu_fwd(const void* gate, const void* up, void* out, int64_t n,
+                                    int32_t dtype, float beta, void* stream) {
+  if (int32_t rc = check_alu(up, n, dtype)) return rc;
+  if (n == 0) return 0;
+  if (gate == nullptr || out == nullptr) return fail("alu_glu: null gate/output");
+  if (int32_t rc = check_aligned({gate, up, out}, "alu_glu")) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  return dtype == ALGX_BF16 ? alu_fwd_any<bf16>(up, gate, out, n, beta, s)
+                            : alu_fwd_any<float>(up, gate, out, n, beta, s);
+}
+
+extern "C" int32_t algx_alu_glu_bwd(const void* gate, const void* up, const void* dout,
+                                    void* dgate, void* dup, int64_t n, int32_t dtype, float beta,
+                                    void* stream) {
+  if (int32_t rc = check_alu(up, n, dtype)) return rc;
+  if (n == 0) return 0;
+  if (gate == nullptr || dout == nullptr || dgate == nullptr || dup == nullptr)
+    return fail("alu_glu: null gate/dout/dgate/dup");
+  if (int32_t rc = check_aligned({gate, up, dout, dgate, dup}, "alu_glu")) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  return dtype == ALGX_BF16 ? alu_bwd_any<bf16>(up, gate, dout, dup, dgate, n, beta, s)
+                            : alu_bwd_any<float>(up, gate, dout, dup, dgate, n, beta, s);
+}

@@ -196,6 +196,45 @@ def bench_qknorm(steps, warmup, dev):
             "bwd_frac": bwd_bytes / b_ms / 1e6 / PEAK_HBM_GBS}
 
 
+def bench_elementwise(steps, warmup, dev):
+    """rms_norm with a gain over 8 x 2048 rows of d_model = 1024 (the 350M
+    model's ln1/ln2), and the fused alu_glu over its (8 x 2048, d_ff = 2688)
+    feed-forward activations: kernel time from the probes, HBM bytes as the
+    operands each kernel must move once."""
+    import torch
+    from algebraic_amd.algebraic import alu_glu, rms_norm
+    gen = torch.Generator(device=dev).manual_seed(4)
+    rows, d, dff = 16384, 1024, 2688
+    x = torch.randn((rows, d), device=dev, generator=gen).bfloat16().requires_grad_(True)
+    g = (1 + 0.1 * torch.randn(d, device=dev, generator=gen)).requires_grad_(True)
+    dy = torch.randn((rows, d), device=dev, generator=gen).bfloat16()
+    gate = torch.randn((rows, dff), device=dev, generator=gen).bfloat16().requires_grad_(True)
+    up = torch.randn((rows, dff), device=dev, generator=gen).bfloat16().requires_grad_(True)
+    dout = torch.randn((rows, dff), device=dev, generator=gen).bfloat16()
+
+    def norm_step():
+        torch.autograd.grad(rms_norm(x, g), (x, g), dy)
+
+    def glu_step():
+        torch.autograd.grad(alu_glu(gate, up, 1.0), (gate, up), dout)
+
+    out = {"workload": f"rms_norm [{rows},{d}] bf16 + f32 gain; alu_glu [{rows},{dff}] bf16"}
+    for name, step, elems, fb, bb in (("rms_norm", norm_step, rows * d, 4, 6),
+                                      ("alu_glu", glu_step, rows * dff, 6, 10)):
+        probe = "rms_norm" if name == "rms_norm" else "alu"
+        fp, bp = Probe(probe + "_fwd", steps), Probe(probe + "_bwd", steps)
+        time_steps(step, steps, warmup, fp)
+        time_steps(step, steps, 1, bp)
+        f_ms, b_ms = fp.mean_ms(), bp.mean_ms()
+        out.update({f"{name}_fwd_us": f_ms * 1e3,
+                    f"{name}_fwd_gbs": elems * fb / f_ms / 1e6,
+                    f"{name}_fwd_frac": elems * fb / f_ms / 1e6 / PEAK_HBM_GBS,
+                    f"{name}_bwd_us": b_ms * 1e3,
+                    f"{name}_bwd_gbs": elems * bb / b_ms / 1e6,
+                    f"{name}_bwd_frac": elems * bb / b_ms / 1e6 / PEAK_HBM_GBS})
+    return out
+
+
 def traffic_bytes():
     """HBM bytes per attention-backward launch measured by rocprofv3 --pmc
     (FETCH_SIZE + WRITE_SIZE, scaled by a 256 MiB copy), when that summary
@@ -229,6 +268,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--head-only", action="store_true",
                     help="time only the fused head (configs[2]) and print its line (for profiling)")
+    ap.add_argument("--elementwise-only", action="store_true",
+                    help="print only the rms_norm / alu_glu line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 256 MiB device copy (scale reference for the "
                          "FETCH_SIZE/WRITE_SIZE counters of a rocprofv3 --pmc run)")
@@ -249,6 +290,11 @@ def main():
     if args.head_only:
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
                           for k, v in bench_head(args.steps, args.warmup, dev).items()}),
+              flush=True)
+        return
+    if args.elementwise_only:
+        print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
+                          for k, v in bench_elementwise(args.steps, args.warmup, dev).items()}),
               flush=True)
         return
     if args.calibrate_copy:
@@ -307,6 +353,8 @@ def main():
                            for k, v in bench_head(5, 2, dev).items()},
             "qknorm": {k: (round(v, 4) if isinstance(v, float) else v)
                        for k, v in bench_qknorm(20, 3, dev).items()},
+            "elementwise": {k: (round(v, 4) if isinstance(v, float) else v)
+                            for k, v in bench_elementwise(20, 3, dev).items()},
         }
     if not args.no_cpu:
         line["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v)

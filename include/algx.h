@@ -11,7 +11,7 @@
  *
  * Layouts are row-major as the reference passes them: attention tensors are
  * (B, H, T, D); the head takes hidden states (N, d) and the tied embedding
- * (V, d); QK-norm takes rows of D=64 values.
+ * (V, d); QK-norm takes rows of D=64 values, rms_norm rows of d_model values.
  */
 #ifndef ALGX_H
 #define ALGX_H
@@ -65,7 +65,11 @@ enum {
   ALGX_PROBE_HEAD_DH = 5,    /* unused: dh runs in the ALGX_PROBE_HEAD_DE launch */
   ALGX_PROBE_HEAD_DE = 6,    /* fused-head dh + dE GEMM launch                 */
   ALGX_PROBE_QKNORM_FWD = 7,
-  ALGX_PROBE_QKNORM_BWD = 8
+  ALGX_PROBE_QKNORM_BWD = 8,
+  ALGX_PROBE_RMSNORM_FWD = 9,
+  ALGX_PROBE_RMSNORM_BWD = 10, /* the row kernel; the dgain finish is not timed  */
+  ALGX_PROBE_ALU_FWD = 11,     /* alu and alu_glu forward                        */
+  ALGX_PROBE_ALU_BWD = 12      /* alu and alu_glu backward                       */
 };
 int32_t algx_set_probe(int32_t which, void* start_event, void* stop_event);
 
@@ -156,6 +160,35 @@ int32_t algx_head_bwd(const void* h, const void* E, const int32_t* targets, cons
                       const float* scale, void* dh, float* dE, void* workspace, int32_t N,
                       int32_t d, int32_t V, int32_t kind, int32_t n, float inv_c, float clamp,
                       int32_t dtype, void* stream);
+
+/* ------------------------------------------------------ elementwise ops
+ * rms_norm (src/algebraic/algebraic.py:76-83) over rows of D values:
+ *   y = cast((x * rsqrt(mean(x^2) + eps)) * gain)
+ * gain: D float32, or NULL for the parameter-free AVN (model.py:142).
+ * x, y, dy, dx: rows x D in dtype, D a multiple of 8 (bf16) or 4 (f32), at most
+ * 1024. The backward is the autodiff VJP of that expression; dgain (D float32)
+ * is written exactly when gain is given, and then needs the workspace. */
+int32_t algx_rms_norm_fwd(const void* x, const float* gain, void* y, int64_t rows, int32_t D,
+                          int32_t dtype, float eps, void* stream);
+int64_t algx_rms_norm_bwd_workspace_bytes(int64_t rows, int32_t D, int32_t dtype);
+int32_t algx_rms_norm_bwd(const void* x, const float* gain, const void* dy, void* dx,
+                          float* dgain, void* workspace, int64_t rows, int32_t D, int32_t dtype,
+                          float eps, void* stream);
+
+/* alu (src/algebraic/algebraic.py:86-117), x/2 (1 + bx / sqrt(1 + b^2 x^2))
+ * computed in float32 and rounded to dtype, with the reference's custom VJP
+ * dx = cast(dy * ((1 + u)/2 + u r^2 / 2)), u = bx r, r = rsqrt(1 + (bx)^2).
+ * n elements, a multiple of 8 (bf16) or 4 (f32). */
+int32_t algx_alu_fwd(const void* x, void* y, int64_t n, int32_t dtype, float beta, void* stream);
+int32_t algx_alu_bwd(const void* x, const void* dy, void* dx, int64_t n, int32_t dtype, float beta,
+                     void* stream);
+/* The alu_glu feed-forward product gate * alu(up) (src/algebraic/model.py:186-191)
+ * in one pass, rounding as the unfused ops do: out = cast(gate * cast(alu(up))).
+ * Backward: dgate = cast(dout * cast(alu(up))), dup = alu VJP of cast(dout * gate). */
+int32_t algx_alu_glu_fwd(const void* gate, const void* up, void* out, int64_t n, int32_t dtype,
+                         float beta, void* stream);
+int32_t algx_alu_glu_bwd(const void* gate, const void* up, const void* dout, void* dgate,
+                         void* dup, int64_t n, int32_t dtype, float beta, void* stream);
 
 #ifdef __cplusplus
 }

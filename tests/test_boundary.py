@@ -6,6 +6,7 @@
   work (flash.py:796-817, fused_head.py:269-272, qk_norm.py:68-75).
 """
 
+import ctypes
 import os
 import re
 
@@ -13,6 +14,7 @@ import pytest
 import torch
 
 from algebraic_amd import _lib
+from algebraic_amd.algebraic import alu, alu_glu, rms_norm
 from algebraic_amd.kernels import flash_attention, fused_head, make_variant, qk_rms_norm
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -44,6 +46,8 @@ def test_host_queries():
     assert _lib.query("algx_qknorm_bwd_workspace_bytes", 1 << 18, 64, 0) > 0
     assert _lib.query("algx_head_fwd_workspace_bytes", 16384, 768, 50304, 0) > 0
     assert _lib.query("algx_head_bwd_workspace_bytes", 16384, 768, 50304, 0) > 0
+    assert _lib.query("algx_rms_norm_bwd_workspace_bytes", 16384, 1024, 0) >= 1024 * 4
+    assert _lib.query("algx_rms_norm_bwd_workspace_bytes", 0, 1024, 0) == 0
 
 
 def test_entry_points_reject_bad_arguments_without_a_gpu():
@@ -57,6 +61,20 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert rc != 0 and b"power of two" in lib.algx_last_error()
     rc = lib.algx_head_fwd(None, None, None, None, None, None, 4, 12, 100, 0, 16, 1.0, 0.0, 0, None)
     assert rc != 0 and b"multiple of 8" in lib.algx_last_error()
+    rc = lib.algx_rms_norm_fwd(None, None, None, 4, 100, 0, 1e-5, None)
+    assert rc != 0 and b"multiple of 8" in lib.algx_last_error()
+    rc = lib.algx_rms_norm_fwd(None, None, None, 4, 2048, 1, 1e-5, None)
+    assert rc != 0 and b"at most 1024" in lib.algx_last_error()
+    rc = lib.algx_rms_norm_bwd(None, None, None, None, None, None, 0, 64, 0, 1e-5, None)
+    assert rc == 0
+    g = ctypes.c_void_p(16)
+    rc = lib.algx_rms_norm_bwd(g, g, g, g, None, None, 4, 64, 0, 1e-5, None)
+    assert rc != 0 and b"dgain" in lib.algx_last_error()
+    rc = lib.algx_alu_fwd(None, None, 16, 2, 1.0, None)
+    assert rc != 0 and b"dtype" in lib.algx_last_error()
+    rc = lib.algx_alu_glu_fwd(ctypes.c_void_p(16), ctypes.c_void_p(24), ctypes.c_void_p(32), 16, 0,
+                              1.0, None)
+    assert rc != 0 and b"16-byte aligned" in lib.algx_last_error()
 
 
 def _t(shape, dtype=torch.bfloat16):
@@ -107,3 +125,22 @@ def test_head_and_norm_validation_mirror_reference():
         qk_rms_norm(_t((1000, 64)), g, block=1024)
     with pytest.raises(ValueError, match="positive"):
         qk_rms_norm(_t((1024, 64)), g, eps=0.0)
+
+
+def test_elementwise_validation():
+    with pytest.raises(NotImplementedError, match="multiple of 8"):
+        rms_norm(_t((4, 100)), None)
+    with pytest.raises(NotImplementedError, match="at most 1024"):
+        rms_norm(_t((4, 2048)), None)
+    with pytest.raises(ValueError, match="gain must have shape"):
+        rms_norm(_t((4, 64)), torch.ones(32))
+    with pytest.raises(ValueError, match="positive"):
+        rms_norm(_t((4, 64)), None, eps=0.0)
+    with pytest.raises(ValueError, match="float32 or bfloat16"):
+        rms_norm(_t((4, 64), torch.float16), None)
+    with pytest.raises(ValueError, match="one dtype"):
+        alu_glu(_t((4, 64)), _t((4, 64), torch.float32))
+    with pytest.raises(ValueError, match="one shape"):
+        alu_glu(_t((4, 64)), _t((4, 32)))
+    with pytest.raises(ValueError, match="one dtype"):
+        alu(_t((4, 64), torch.float64))
