@@ -304,9 +304,12 @@ int bwd_blocks(int64_t rows) {
   return (int)(nb > kMaxBwdBlocks ? kMaxBwdBlocks : nb);
 }
 
+// One 16-byte vector per thread and no grid-stride loop (up to 2^30 groups):
+// workgroups then sweep the operands in address order, which streams from HBM
+// faster than a capped grid striding over the whole range.
 int elt_blocks(int64_t nvec) {
   int64_t nb = (nvec + kEltThreads - 1) / kEltThreads;
-  return (int)(nb > 8192 ? 8192 : nb);
+  return (int)(nb > (1 << 30) ? (1 << 30) : nb);
 }
 
 int epl_of(int dtype) { return dtype == ALGX_BF16 ? 8 : 4; }
