@@ -235,6 +235,49 @@ def bench_elementwise(steps, warmup, dev):
     return out
 
 
+def model_flops_per_token(cfg, T):
+    """Training FLOPs per token without rematerialisation: 6 x the block and
+    head parameters' MACs, plus 3.5 x the causal attention forward
+    (2 H T D per layer and token)."""
+    d, f, L, V, H, D = cfg.d_model, cfg.d_ff, cfg.n_layers, cfg.vocab_size, cfg.n_heads, cfg.head_dim
+    dense = L * (4 * d * d + 3 * d * f) + d * V
+    return 6 * dense + 3.5 * L * 2 * H * T * D
+
+
+def bench_model(preset, steps, warmup, dev, B=8, T=2048, V=50304):
+    """one forward + backward of the 350M preset (d 1024, 24 layers,
+    16 heads of 64, d_ff 2688, V 50304) on B x T random tokens, random-init
+    weights, bf16, rematerialised blocks; parameter gradients are produced
+    (no optimiser update)."""
+    import torch
+    from algebraic_amd import config, model
+    cfg = config.build(preset, "350m", vocab_size=V, seq_len=T, attn_impl="flash",
+                       head_impl="fused")
+    params = model.init_params(cfg, seed=0, device=dev)
+    leaves = list(model._leaves(params))
+    gen = torch.Generator(device=dev).manual_seed(5)
+    tok = torch.randint(0, V, (B, T + 1), generator=gen, device=dev)
+    x, y = tok[:, :-1].contiguous(), tok[:, 1:].contiguous()
+    tables = model.position_tables(cfg, T, device=dev)
+
+    def step():
+        for t in leaves:
+            t.grad = None
+        obj, _ = model.train_objective(params, x, y, cfg, tables)
+        obj.backward()
+
+    dt = time_steps(step, steps, warmup)
+    fpt = model_flops_per_token(cfg, T)
+    out = {"workload": f"configs[4] {preset} 350M fwd+bwd, B={B}, T={T}, V={V}, bf16, remat",
+           "ms_per_step": dt * 1e3, "tokens_per_s": B * T / dt,
+           "tflops": fpt * B * T / dt / 1e12, "flops_per_token": fpt,
+           "frac": fpt * B * T / dt / 1e12 / PEAK_BF16_TFLOPS,
+           "params": model.count_params(params)}
+    del params, leaves
+    torch.cuda.empty_cache()
+    return out
+
+
 def traffic_bytes():
     """HBM bytes per attention-backward launch measured by rocprofv3 --pmc
     (FETCH_SIZE + WRITE_SIZE, scaled by a 256 MiB copy), when that summary
@@ -268,6 +311,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--head-only", action="store_true",
                     help="time only the fused head (configs[2]) and print its line (for profiling)")
+    ap.add_argument("--model-only", action="store_true",
+                    help="print only the 350M model lines (algebraic and standard)")
     ap.add_argument("--elementwise-only", action="store_true",
                     help="print only the rms_norm / alu_glu line")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -291,6 +336,12 @@ def main():
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
                           for k, v in bench_head(args.steps, args.warmup, dev).items()}),
               flush=True)
+        return
+    if args.model_only:
+        for preset in ("algebraic", "standard"):
+            print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
+                              for k, v in bench_model(preset, args.steps, args.warmup,
+                                                      dev).items()}), flush=True)
         return
     if args.elementwise_only:
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
@@ -356,6 +407,10 @@ def main():
             "elementwise": {k: (round(v, 4) if isinstance(v, float) else v)
                             for k, v in bench_elementwise(20, 3, dev).items()},
         }
+        for preset in ("algebraic", "standard"):
+            line["secondary"][f"model_350m_{preset}"] = {
+                k: (round(v, 4) if isinstance(v, float) else v)
+                for k, v in bench_model(preset, 5, 2, dev).items()}
     if not args.no_cpu:
         line["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                 for k, v in cpu_baseline(B, H, T, D).items()}
