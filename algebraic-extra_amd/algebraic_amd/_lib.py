@@ -62,6 +62,11 @@ SIGNATURES = {
     "algx_alu_bwd": (_i32, [_p, _p, _p, _i64, _i32, _f32, _p]),
     "algx_alu_glu_fwd": (_i32, [_p, _p, _p, _i64, _i32, _f32, _p]),
     "algx_alu_glu_bwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _f32, _p]),
+    "algx_qk_prologue_fwd": (_i32, [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,
+                                    _i32, _i32, _i32, _f32, _p]),
+    "algx_qk_prologue_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32]),
+    "algx_qk_prologue_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p,
+                                    _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _p]),
 }
 
 _lib = None
@@ -99,6 +104,11 @@ def query(name, *args):
 def ptr(t):
     """Device pointer of a tensor (or None)."""
     return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def c_ptr(address):
+    """A raw device address (an offset into a tensor) as a pointer argument."""
+    return ctypes.c_void_p(address)
 
 
 def stream():

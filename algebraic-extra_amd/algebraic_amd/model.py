@@ -6,9 +6,11 @@ tables, block and head, so that the reference's presets
 (``algebraic_amd.config``) build the same architectures. The path's operators
 run as HIP kernels of libalgx.so: attention (``flash_attention``, both
 ``attn_impl`` values), QK-norm, the RMS norms, the ALU-GLU feed-forward
-product and, with ``head_impl="fused"``, the LM head + loss. The projections
-are plain bf16 GEMMs (hipBLASLt through torch); the rotation tables, the
-rotate-half product, SwiGLU's ``silu`` and the dense head are torch ops.
+product, the attention prologue (QK-norm, rotation and the layout change in
+one pass, for 64-wide heads) and, with ``head_impl="fused"``, the LM head +
+loss. The projections are plain bf16 GEMMs (hipBLASLt through torch); the
+rotation tables, SwiGLU's ``silu``, the dense head and, for other head
+widths, the rotate-half product are torch ops.
 
 ``remat=True`` recomputes each block in the backward
 (``torch.utils.checkpoint``), as ``jax.checkpoint`` does (model.py:205-206).
@@ -25,6 +27,7 @@ from torch.utils.checkpoint import checkpoint
 from .algebraic import alu_glu, rms_norm
 from .kernels.flash import flash_attention
 from .kernels.fused_head import fused_head
+from .kernels.prologue import attention_prologue
 from .kernels.qk_norm import qk_rms_norm
 
 F32 = torch.float32
@@ -256,20 +259,37 @@ def _attention(q, k, v, sink_logit, cfg: LMConfig):
                            block=cfg.flash_block, range_guard=cfg.attn == "asinh")
 
 
-def _block(cfg: LMConfig, cos, sin, x, lp):
-    """One pre-norm block (model.py:162-191)."""
-    B, T, d = x.shape
+def _qkv(cfg: LMConfig, cos, sin, h, lp):
+    """q, k, v in (B, H, T, D) ready for attention (model.py:166-174).
+
+    With D = 64 one GEMM against [w_q | w_k | w_v] feeds the fused prologue
+    kernel (QK-norm, rotation and the layout change in one pass over the
+    projections); other head widths take the operators one by one."""
+    B, T, d = h.shape
     H, D = cfg.n_heads, cfg.head_dim
-    dt = x.dtype
-    h = _norm(x, lp.get("ln1"), cfg)
+    dt = h.dtype
+    if D == 64:
+        w = torch.cat([lp["w_q"], lp["w_k"], lp["w_v"]], dim=1).to(dt)
+        qkv = h @ w
+        gains = (lp["q_gain"], lp["k_gain"]) if cfg.qk_norm else (None, None)
+        tabs = (None, None) if cfg.pos == "none" else (cos, sin)
+        return attention_prologue(qkv, H, gains[0], gains[1], tabs[0], tabs[1], cfg.eps)
     q = (h @ lp["w_q"].to(dt)).view(B, T, H, D).transpose(1, 2)
     k = (h @ lp["w_k"].to(dt)).view(B, T, H, D).transpose(1, 2)
     v = (h @ lp["w_v"].to(dt)).view(B, T, H, D).transpose(1, 2)
     if cfg.qk_norm:
         q = _qk_norm(q, lp["q_gain"], cfg)
         k = _qk_norm(k, lp["k_gain"], cfg)
-    q = apply_rotary(q, cos, sin)
-    k = apply_rotary(k, cos, sin)
+    return apply_rotary(q, cos, sin), apply_rotary(k, cos, sin), v
+
+
+def _block(cfg: LMConfig, cos, sin, x, lp):
+    """One pre-norm block (model.py:162-191)."""
+    B, T, d = x.shape
+    H = cfg.n_heads
+    dt = x.dtype
+    h = _norm(x, lp.get("ln1"), cfg)
+    q, k, v = _qkv(cfg, cos, sin, h, lp)
     if cfg.sink == "learned":
         sink = lp["sink"].to(F32)
     elif cfg.sink == "const":
@@ -296,9 +316,12 @@ def forward_hidden(params, tokens: torch.Tensor, cfg: LMConfig, tables) -> torch
     cos, sin = tables
     x = F.embedding(tokens, params["embed"]).to(cfg.compute_dtype)
     x = _norm(x, params.get("embed_gain"), cfg)
-    layers = params["layers"]
+    # One unbind per stacked leaf: its backward stacks the per-layer gradients
+    # in one pass, where indexing t[i] per layer would materialise (and add)
+    # a zero-filled full-size gradient for every layer.
+    per_layer = {name: t.unbind(0) for name, t in params["layers"].items()}
     for i in range(cfg.n_layers):
-        lp = {name: t[i] for name, t in layers.items()}
+        lp = {name: ts[i] for name, ts in per_layer.items()}
         if cfg.remat:
             x = checkpoint(_block, cfg, cos, sin, x, lp, use_reentrant=False)
         else:

@@ -190,6 +190,33 @@ int32_t algx_alu_glu_fwd(const void* gate, const void* up, void* out, int64_t n,
 int32_t algx_alu_glu_bwd(const void* gate, const void* up, const void* dout, void* dgate,
                          void* dup, int64_t n, int32_t dtype, float beta, void* stream);
 
+/* ------------------------------------------------------ attention prologue
+ * The model block's step from projections to attention inputs
+ * (src/algebraic/model.py:166-174) in one pass: q, k, v are rows of the
+ * (B, T, *) projection output with row stride ld elements (they may point
+ * into one fused (B, T, 3 H D) buffer); writes, in (B, H, T, D),
+ *   q_out = rotate(cast(rms_norm(q, q_gain))), k_out likewise, v_out = v
+ * where rms_norm is algebraic.py:76-83 and rotate the rotate-half product of
+ * algebraic.py:172-179 with cos, sin: (T, D/2) float32 tables, rounded to
+ * dtype after every product and sum as the reference's ops are. D = 64.
+ * q_gain = k_gain = NULL skips the norm (qk_norm off); cos = sin = NULL skips
+ * the rotation. The backward writes dq, dk, dv into projection-gradient rows
+ * (stride ld) and, with gains, dq_gain and dk_gain (64 float32 each; needs
+ * the workspace). */
+int32_t algx_qk_prologue_fwd(const void* q, const void* k, const void* v, int64_t ld,
+                             const float* q_gain, const float* k_gain, const float* cos_t,
+                             const float* sin_t, void* q_out, void* k_out, void* v_out, int32_t B,
+                             int32_t T, int32_t H, int32_t D, int32_t dtype, float eps,
+                             void* stream);
+int64_t algx_qk_prologue_bwd_workspace_bytes(int32_t B, int32_t T, int32_t H, int32_t D,
+                                             int32_t dtype);
+int32_t algx_qk_prologue_bwd(const void* q, const void* k, const float* q_gain, const float* k_gain,
+                             const float* cos_t, const float* sin_t, const void* dq_out,
+                             const void* dk_out, const void* dv_out, void* dq, void* dk, void* dv,
+                             int64_t ld, float* dq_gain, float* dk_gain, void* workspace,
+                             int32_t B, int32_t T, int32_t H, int32_t D, int32_t dtype, float eps,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,7 +1,7 @@
 """The model over the HIP operators against the float64 model oracle (GPU).
 
-A small model of each preset (d_model 64, 2 layers, 2 heads of 32, d_ff 96,
-V = 97, T = 16; weights at init_std 0.1 with perturbed gains and sink logits
+A small model of each preset (2 layers, 2 heads of 32 or 64 -- the latter
+through the fused attention prologue --, d_ff 96, V = 97, T = 16; weights at init_std 0.1 with perturbed gains and sink logits
 so every path carries signal) runs one forward + backward; its objective,
 telemetry and every parameter gradient are compared with torch float64
 autograd of ``oracle.model`` on the same parameters and tokens.
@@ -33,8 +33,9 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _cfg(preset, dtype, head_impl, **kw):
-    return config.build(preset, "proxy", d_model=64, n_layers=2, n_heads=2, d_ff=96,
+def _cfg(preset, dtype, head_impl, head_dim=32, **kw):
+    # head_dim 64 takes the fused attention prologue, 32 the operators one by one
+    return config.build(preset, "proxy", d_model=2 * head_dim, n_layers=2, n_heads=2, d_ff=96,
                         vocab_size=97, seq_len=16, init_std=0.1, dtype=dtype,
                         head_impl=head_impl, attn_impl="flash", **kw)
 
@@ -85,13 +86,14 @@ def _run(cfg, seed=0):
     return params, obj, tel, ref, r_obj, r_tel
 
 
+@pytest.mark.parametrize("head_dim", [32, 64])
 @pytest.mark.parametrize("preset", ["algebraic", "standard"])
 @pytest.mark.parametrize("dtype,head_impl,grad_tol,obj_tol", [
     ("float32", "dense", 1e-4, 1e-5),
     ("bfloat16", "fused", 3e-2, 1e-2),
 ])
-def test_small_model_matches_oracle(preset, dtype, head_impl, grad_tol, obj_tol):
-    cfg = _cfg(preset, dtype, head_impl)
+def test_small_model_matches_oracle(preset, dtype, head_impl, grad_tol, obj_tol, head_dim):
+    cfg = _cfg(preset, dtype, head_impl, head_dim)
     params, obj, tel, ref, r_obj, r_tel = _run(cfg)
     assert abs(float(obj.detach()) - float(r_obj.detach())) <= obj_tol * abs(float(r_obj.detach()))
     assert rel_l2(tel, r_tel) <= obj_tol * 10

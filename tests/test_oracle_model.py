@@ -135,3 +135,32 @@ def test_presets_and_parameter_count():
     want = 97 * 64 + 2 * (4 * 64 * 64 + 3 * 64 * 96) + 2 * 64 + 2 * 2 * 64 + 2 * 2 * 32 + 2 * 2
     assert model.count_params(p) == want
     assert model.decay_mask(p)["layers"]["w_q"] and not model.decay_mask(p)["layers"]["ln1"]
+
+
+def test_prologue_oracle_rotation_is_complex_multiplication_and_vjp_is_autograd():
+    """Rotate-half = (x1 + i x2) e^{i phi}; the whole chain's VJP equals torch
+    float64 autograd of norm -> rotation -> transpose."""
+    from oracle import prologue as OP
+    rng = np.random.default_rng(9)
+    B, T, H, D = 2, 5, 3, 64
+    x = rng.standard_normal((B, T, H, D)) * 2
+    gain = 0.5 + rng.random(D)
+    phi = rng.random((T, D // 2)) * 6
+    cos, sin = np.cos(phi), np.sin(phi)
+    got = OP.forward(x, None, cos, sin, 1e-5, "f64")
+    z = (x[..., :32] + 1j * x[..., 32:]) * np.exp(1j * phi)[None, :, None, :]
+    np.testing.assert_allclose(got, np.transpose(np.concatenate([z.real, z.imag], -1),
+                                                 (0, 2, 1, 3)), atol=1e-12)
+    dout = rng.standard_normal((B, H, T, D))
+    tx = torch.tensor(x, requires_grad=True)
+    tg = torch.tensor(gain, requires_grad=True)
+    y = tx / torch.sqrt((tx * tx).mean(-1, keepdim=True) + 1e-5) * tg
+    c, s = torch.tensor(cos)[None, :, None, :], torch.tensor(sin)[None, :, None, :]
+    y = torch.cat([y[..., :32] * c - y[..., 32:] * s, y[..., :32] * s + y[..., 32:] * c], -1)
+    out = y.transpose(1, 2)
+    (out * torch.tensor(dout)).sum().backward()
+    np.testing.assert_allclose(OP.forward(x, gain, cos, sin, 1e-5, "f64"),
+                               out.detach().numpy(), rtol=1e-12, atol=1e-12)
+    dx, dg = OP.backward(x, gain, cos, sin, dout, 1e-5, "f64")
+    np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dg, tg.grad.numpy(), rtol=1e-6)
