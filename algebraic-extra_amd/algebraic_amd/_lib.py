@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libalgx.so"
 BF16, F32 = 0, 1
 SOFTMAX, ASINH = 0, 1
 HEAD_CE, HEAD_ALG_CE = 0, 1
+GLU_ALU, GLU_SILU = 0, 1
 PROBE = {"none": 0, "attn_fwd": 1, "attn_bwd": 2, "head_fwd": 3, "head_dz": 4, "head_dh": 5,
          "head_de": 6, "qknorm_fwd": 7, "qknorm_bwd": 8, "rms_norm_fwd": 9, "rms_norm_bwd": 10,
          "alu_fwd": 11, "alu_bwd": 12}
@@ -62,6 +63,8 @@ SIGNATURES = {
     "algx_alu_bwd": (_i32, [_p, _p, _p, _i64, _i32, _f32, _p]),
     "algx_alu_glu_fwd": (_i32, [_p, _p, _p, _i64, _i32, _f32, _p]),
     "algx_alu_glu_bwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _f32, _p]),
+    "algx_glu_packed_fwd": (_i32, [_p, _p, _i64, _i32, _i32, _i32, _f32, _p]),
+    "algx_glu_packed_bwd": (_i32, [_p, _p, _p, _i64, _i32, _i32, _i32, _f32, _p]),
     "algx_qk_prologue_fwd": (_i32, [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,
                                     _i32, _i32, _i32, _f32, _p]),
     "algx_qk_prologue_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32]),

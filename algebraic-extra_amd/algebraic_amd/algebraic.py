@@ -135,3 +135,45 @@ def alu_glu(gate: torch.Tensor, up: torch.Tensor, beta: float = 1.0) -> torch.Te
     if gate.shape != up.shape:
         raise ValueError("alu_glu needs gate and up of one shape")
     return _ALUGLUFn.apply(_aligned(gate), _aligned(up), float(beta))
+
+
+class _GLUPackedFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gu, act, beta):
+        cols = gu.shape[-1] // 2
+        rows = gu.numel() // (2 * cols)
+        y = torch.empty(gu.shape[:-1] + (cols,), dtype=gu.dtype, device=gu.device)
+        code = _lib.GLU_ALU if act == "alu" else _lib.GLU_SILU
+        _lib.call("algx_glu_packed_fwd", _lib.ptr(gu), _lib.ptr(y), rows, cols, code,
+                  _lib.dtype_code(gu.dtype), float(beta), _lib.stream())
+        ctx.cfg = (code, beta)
+        ctx.save_for_backward(gu)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (gu,) = ctx.saved_tensors
+        code, beta = ctx.cfg
+        cols = gu.shape[-1] // 2
+        rows = gu.numel() // (2 * cols)
+        dy = _aligned(dy.to(gu.dtype))
+        dgu = torch.empty_like(gu)
+        _lib.call("algx_glu_packed_bwd", _lib.ptr(gu), _lib.ptr(dy), _lib.ptr(dgu), rows, cols,
+                  code, _lib.dtype_code(gu.dtype), float(beta), _lib.stream())
+        return dgu, None, None
+
+
+def glu_packed(gu: torch.Tensor, act: str = "alu", beta: float = 1.0) -> torch.Tensor:
+    """``gate * act(up)`` for ``gu = [gate | up]`` on the last axis (one GEMM
+    against ``[w_g | w_u]``, model.py:184-191): ``act="alu"`` is
+    ``alu(up, beta)``, ``act="silu"`` is SwiGLU's ``up * sigmoid(up)``
+    (standard.py:12-13). The gradient comes back packed the same way."""
+    _check_float(gu)
+    if act not in ("alu", "silu"):
+        raise ValueError(f"unknown activation {act!r}")
+    if gu.shape[-1] % 2:
+        raise ValueError("glu_packed needs an even last axis [gate | up]")
+    width = 8 if gu.dtype == torch.bfloat16 else 4
+    if (gu.shape[-1] // 2) % width:
+        raise NotImplementedError(f"glu_packed needs gate/up widths that are a multiple of {width}")
+    return _GLUPackedFn.apply(_aligned(gu), act, float(beta))

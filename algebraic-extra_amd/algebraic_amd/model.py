@@ -6,11 +6,12 @@ tables, block and head, so that the reference's presets
 (``algebraic_amd.config``) build the same architectures. The path's operators
 run as HIP kernels of libalgx.so: attention (``flash_attention``, both
 ``attn_impl`` values), QK-norm, the RMS norms, the ALU-GLU feed-forward
-product, the attention prologue (QK-norm, rotation and the layout change in
-one pass, for 64-wide heads) and, with ``head_impl="fused"``, the LM head +
-loss. The projections are plain bf16 GEMMs (hipBLASLt through torch); the
-rotation tables, SwiGLU's ``silu``, the dense head and, for other head
-widths, the rotate-half product are torch ops.
+product (and SwiGLU's), the attention prologue (QK-norm, rotation and the
+layout change in one pass, for 64-wide heads) and, with
+``head_impl="fused"``, the LM head + loss. The projections are plain bf16
+GEMMs (hipBLASLt through torch), with q/k/v and gate/up each fused into one
+GEMM; the rotation tables, the dense head and, for other head widths, the
+rotate-half product are torch ops.
 
 ``remat=True`` recomputes each block in the backward
 (``torch.utils.checkpoint``), as ``jax.checkpoint`` does (model.py:205-206).
@@ -24,7 +25,7 @@ import torch
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
-from .algebraic import alu_glu, rms_norm
+from .algebraic import glu_packed, rms_norm
 from .kernels.flash import flash_attention
 from .kernels.fused_head import fused_head
 from .kernels.prologue import attention_prologue
@@ -300,14 +301,12 @@ def _block(cfg: LMConfig, cos, sin, x, lp):
     a = a.transpose(1, 2).reshape(B, T, d)
     x = x + a @ lp["w_o"].to(dt)
     h2 = _norm(x, lp.get("ln2"), cfg)
-    gate = h2 @ lp["w_g"].to(dt)
-    up = h2 @ lp["w_u"].to(dt)
-    if cfg.ffn == "swiglu":
-        y = gate * F.silu(up)
-    elif cfg.ffn == "alu_glu":
-        y = alu_glu(gate, up, cfg.alu_beta)
-    else:
+    if cfg.ffn not in ("swiglu", "alu_glu"):
         raise ValueError(f"unknown ffn {cfg.ffn!r}")
+    # gate and up from one GEMM against [w_g | w_u]; the gated product reads
+    # its rows in place and returns the gradient packed the same way.
+    gu = h2 @ torch.cat([lp["w_g"], lp["w_u"]], dim=1).to(dt)
+    y = glu_packed(gu, "alu" if cfg.ffn == "alu_glu" else "silu", cfg.alu_beta)
     return x + y @ lp["w_d"].to(dt)
 
 

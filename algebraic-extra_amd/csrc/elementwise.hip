@@ -491,3 +491,152 @@ extern "C" int32_t algx_alu_glu_bwd(const void* gate, const void* up, const void
   return dtype == ALGX_BF16 ? alu_bwd_any<bf16>(up, gate, dout, dup, dgate, n, beta, s)
                             : alu_bwd_any<float>(up, gate, dout, dup, dgate, n, beta, s);
 }
+
+// ---------------------------------------------------------------------------
+// Gated feed-forward on the packed projection [gate | up] (rows x 2 cols):
+// the model's gate and up GEMMs (model.py:184-185) as one GEMM against
+// [w_g | w_u], and the gated product read straight from its output rows.
+// ACT = ALGX_GLU_ALU: gate * alu(up) exactly as algx_alu_glu_*;
+// ACT = ALGX_GLU_SILU: gate * silu(up), silu(x) = x * sigmoid(x)
+// (standard.py:12-13) with sigmoid rounded to dtype before the product as the
+// reference's bf16 ops round; its VJP uses sigma + x sigma (1 - sigma) in
+// float32.
+namespace algx {
+namespace {
+
+__device__ __forceinline__ float sigmoid_f(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
+template <typename T, int ACT>
+__global__ __launch_bounds__(kEltThreads) void glu_packed_fwd_kernel(const T* __restrict__ gu,
+                                                                     T* __restrict__ y,
+                                                                     int64_t nvec, int nvr,
+                                                                     int cols, float beta) {
+  typedef typename Vec<T>::type VT;
+  constexpr int EPL = Vec<T>::n;
+  const int64_t i = (int64_t)blockIdx.x * kEltThreads + threadIdx.x;
+  if (i >= nvec) return;
+  const int64_t r = i / nvr;
+  const int c = (int)(i - r * nvr) * EPL;
+  const VT gv = *reinterpret_cast<const VT*>(gu + r * 2 * cols + c);
+  const VT uv = *reinterpret_cast<const VT*>(gu + r * 2 * cols + cols + c);
+  VT out;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float up = to_f(uv[e]);
+    float act;
+    if (ACT == ALGX_GLU_ALU) {
+      float u, rr;
+      act = round_to<T>(alu_parts(up, beta, u, rr));
+    } else {
+      act = round_to<T>(up * round_to<T>(sigmoid_f(up)));
+    }
+    out[e] = from_f<T>(to_f(gv[e]) * act);
+  }
+  *reinterpret_cast<VT*>(y + r * cols + c) = out;
+}
+
+template <typename T, int ACT>
+__global__ __launch_bounds__(kEltThreads) void glu_packed_bwd_kernel(const T* __restrict__ gu,
+                                                                     const T* __restrict__ dy,
+                                                                     T* __restrict__ dgu,
+                                                                     int64_t nvec, int nvr,
+                                                                     int cols, float beta) {
+  typedef typename Vec<T>::type VT;
+  constexpr int EPL = Vec<T>::n;
+  const int64_t i = (int64_t)blockIdx.x * kEltThreads + threadIdx.x;
+  if (i >= nvec) return;
+  const int64_t r = i / nvr;
+  const int c = (int)(i - r * nvr) * EPL;
+  const VT gv = *reinterpret_cast<const VT*>(gu + r * 2 * cols + c);
+  const VT uv = *reinterpret_cast<const VT*>(gu + r * 2 * cols + cols + c);
+  const VT dv = *reinterpret_cast<const VT*>(dy + r * cols + c);
+  VT dg, du;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float up = to_f(uv[e]), g = to_f(dv[e]);
+    const float gact = round_to<T>(g * to_f(gv[e]));
+    float act, deriv;
+    if (ACT == ALGX_GLU_ALU) {
+      float u, rr;
+      act = round_to<T>(alu_parts(up, beta, u, rr));
+      deriv = alu_deriv(u, rr);
+    } else {
+      const float sg = sigmoid_f(up);
+      act = round_to<T>(up * round_to<T>(sg));
+      deriv = __builtin_fmaf(up * sg, 1.0f - sg, sg);
+    }
+    dg[e] = from_f<T>(g * act);
+    du[e] = from_f<T>(gact * deriv);
+  }
+  *reinterpret_cast<VT*>(dgu + r * 2 * cols + c) = dg;
+  *reinterpret_cast<VT*>(dgu + r * 2 * cols + cols + c) = du;
+}
+
+int32_t check_packed(const void* gu, int64_t rows, int32_t cols, int32_t act, int32_t dtype) {
+  if (dtype != ALGX_BF16 && dtype != ALGX_F32) return fail("glu_packed: dtype must be bf16 or f32");
+  if (act != ALGX_GLU_ALU && act != ALGX_GLU_SILU) return fail("glu_packed: unknown activation");
+  if (rows < 0 || cols <= 0 || cols % epl_of(dtype))
+    return fail("glu_packed: cols must be a positive multiple of 8 (bf16) or 4 (f32)");
+  if (rows > 0 && gu == nullptr) return fail("glu_packed: null input");
+  return 0;
+}
+
+template <typename T>
+void glu_packed_fwd_any(const void* gu, void* y, int64_t rows, int cols, int act, float beta,
+                        hipStream_t s) {
+  const int nvr = cols / Vec<T>::n;
+  const int64_t nvec = rows * nvr;
+  const dim3 grid((unsigned)((nvec + kEltThreads - 1) / kEltThreads));
+  const Probe probe = probe_for(ALGX_PROBE_ALU_FWD);
+  if (act == ALGX_GLU_ALU)
+    launch_k(probe, glu_packed_fwd_kernel<T, ALGX_GLU_ALU>, grid, dim3(kEltThreads), s,
+             (const T*)gu, (T*)y, nvec, nvr, cols, beta);
+  else
+    launch_k(probe, glu_packed_fwd_kernel<T, ALGX_GLU_SILU>, grid, dim3(kEltThreads), s,
+             (const T*)gu, (T*)y, nvec, nvr, cols, beta);
+}
+
+template <typename T>
+void glu_packed_bwd_any(const void* gu, const void* dy, void* dgu, int64_t rows, int cols, int act,
+                        float beta, hipStream_t s) {
+  const int nvr = cols / Vec<T>::n;
+  const int64_t nvec = rows * nvr;
+  const dim3 grid((unsigned)((nvec + kEltThreads - 1) / kEltThreads));
+  const Probe probe = probe_for(ALGX_PROBE_ALU_BWD);
+  if (act == ALGX_GLU_ALU)
+    launch_k(probe, glu_packed_bwd_kernel<T, ALGX_GLU_ALU>, grid, dim3(kEltThreads), s,
+             (const T*)gu, (const T*)dy, (T*)dgu, nvec, nvr, cols, beta);
+  else
+    launch_k(probe, glu_packed_bwd_kernel<T, ALGX_GLU_SILU>, grid, dim3(kEltThreads), s,
+             (const T*)gu, (const T*)dy, (T*)dgu, nvec, nvr, cols, beta);
+}
+
+}  // namespace
+}  // namespace algx
+
+extern "C" int32_t algx_glu_packed_fwd(const void* gu, void* y, int64_t rows, int32_t cols,
+                                       int32_t act, int32_t dtype, float beta, void* stream) {
+  if (int32_t rc = check_packed(gu, rows, cols, act, dtype)) return rc;
+  if (rows == 0) return 0;
+  if (y == nullptr) return fail("glu_packed: null output");
+  if (int32_t rc = check_aligned({gu, y}, "glu_packed")) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ALGX_BF16) glu_packed_fwd_any<bf16>(gu, y, rows, cols, act, beta, s);
+  else glu_packed_fwd_any<float>(gu, y, rows, cols, act, beta, s);
+  return check_launch("glu_packed_fwd");
+}
+
+extern "C" int32_t algx_glu_packed_bwd(const void* gu, const void* dy, void* dgu, int64_t rows,
+                                       int32_t cols, int32_t act, int32_t dtype, float beta,
+                                       void* stream) {
+  if (int32_t rc = check_packed(gu, rows, cols, act, dtype)) return rc;
+  if (rows == 0) return 0;
+  if (dy == nullptr || dgu == nullptr) return fail("glu_packed: null dy/dgu");
+  if (int32_t rc = check_aligned({gu, dy, dgu}, "glu_packed")) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ALGX_BF16) glu_packed_bwd_any<bf16>(gu, dy, dgu, rows, cols, act, beta, s);
+  else glu_packed_bwd_any<float>(gu, dy, dgu, rows, cols, act, beta, s);
+  return check_launch("glu_packed_bwd");
+}

@@ -11,12 +11,11 @@
 //
 // D = 64. A row (b, t, h) is 128 bytes in bf16: 8 lanes of 16 bytes (16
 // lanes in f32). The rotate-half partner of a lane's elements sits in lane
-// ^ (lanes per row / 2), one xor-shuffle away. A workgroup owns one of q, k,
-// v for one (b, h) and 512 consecutive tokens (128 per wave), so its writes
-// in the (B, H, T, D) layout are one contiguous 64 KB stretch and its reads
-// are the 128-byte head slices of 512 consecutive projection rows. The gain
-// gradients are reduced per workgroup and finished per column in a fixed
-// order.
+// ^ (lanes per row / 2), one xor-shuffle away. A workgroup owns 16 tokens of
+// one sequence and every head slice of their q, k and v rows, so it reads
+// whole projection rows and writes 2 KB runs of the (B, H, T, D) outputs.
+// The gain gradients are reduced per workgroup and finished per column in a
+// fixed order.
 #include "common.h"
 
 namespace algx {
@@ -25,8 +24,8 @@ namespace {
 
 constexpr int kD = 64;
 constexpr int kThreads = 256;
-constexpr int kWaveTokens = 128;
-constexpr int kSegTokens = kWaveTokens * (kThreads / 64);
+constexpr int kWaves = kThreads / 64;
+constexpr int kBlockTokens = 16;
 
 template <typename T> struct Vec;
 template <> struct Vec<bf16> { typedef bf16x8 type; static constexpr int n = 8; };
@@ -38,94 +37,80 @@ template <int LPR> __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-struct Seg {
-  int which, b, h, t0;
-};
-
-// Workgroup -> (which of q/k/v, b, h, 512-token segment); waves take 128
-// tokens each.
-__device__ __forceinline__ Seg seg_of(int B, int H, int nseg) {
-  int r = blockIdx.x;
-  Seg s;
-  const int seg = r % nseg;
-  r /= nseg;
-  s.h = r % H;
-  r /= H;
-  s.b = r % B;
-  s.which = r / B;
-  s.t0 = seg * kSegTokens + (threadIdx.x >> 6) * kWaveTokens;
-  return s;
-}
-
+// A workgroup owns 16 consecutive tokens of one sequence and all 3 H head
+// slices of their projection rows (q heads, then k, then v): it reads whole
+// rows, and each (slice, 16 tokens) it writes is one contiguous 2 KB run of
+// the (B, H, T, D) output. Wave w takes slices w, w + 4, ...
 template <typename T, bool NORM, bool ROT>
 __global__ __launch_bounds__(kThreads) void prologue_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, int64_t ld,
     const float* __restrict__ q_gain, const float* __restrict__ k_gain,
     const float* __restrict__ cosb, const float* __restrict__ sinb, T* __restrict__ q_out,
-    T* __restrict__ k_out, T* __restrict__ v_out, int B, int Tn, int H, int nseg, float eps) {
+    T* __restrict__ k_out, T* __restrict__ v_out, int Tn, int H, int ntb, float eps) {
   typedef typename Vec<T>::type VT;
   constexpr int EPL = Vec<T>::n;
   constexpr int LPR = kD / EPL;
   constexpr int RPW = 64 / LPR;
   constexpr int HALF = LPR / 2;
-  const Seg sg = seg_of(B, H, nseg);
-  const int lane = threadIdx.x & 63, sub = lane % LPR, rw = lane / LPR;
-  const T* src = sg.which == 0 ? q : (sg.which == 1 ? k : v);
-  T* dst = sg.which == 0 ? q_out : (sg.which == 1 ? k_out : v_out);
-  src += (int64_t)sg.b * Tn * ld + sg.h * kD + sub * EPL;
-  dst += ((int64_t)sg.b * H + sg.h) * Tn * kD + sub * EPL;
-  if (sg.which == 2) {
-    for (int i = 0; i < kWaveTokens; i += RPW) {
-      const int t = sg.t0 + i + rw;
-      if (t < Tn)
-        *reinterpret_cast<VT*>(dst + (int64_t)t * kD) =
-            *reinterpret_cast<const VT*>(src + (int64_t)t * ld);
-    }
-    return;
-  }
-  float g[EPL];
-  const float* gain = sg.which == 0 ? q_gain : k_gain;
+  const int b = blockIdx.x / ntb, t0 = (blockIdx.x % ntb) * kBlockTokens;
+  const int lane = threadIdx.x & 63, sub = lane % LPR, rw = lane / LPR, w = threadIdx.x >> 6;
+  float gq[EPL], gk[EPL];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) g[e] = NORM ? gain[sub * EPL + e] : 1.0f;
+  for (int e = 0; e < EPL; ++e) {
+    gq[e] = NORM ? q_gain[sub * EPL + e] : 1.0f;
+    gk[e] = NORM ? k_gain[sub * EPL + e] : 1.0f;
+  }
   const int j0 = (sub % HALF) * EPL;
   const bool first = sub < HALF;
-#pragma unroll 2
-  for (int i = 0; i < kWaveTokens; i += RPW) {
-    const int t = sg.t0 + i + rw;
-    const bool ok = t < Tn;
-    VT xin;
-    if (ok) xin = *reinterpret_cast<const VT*>(src + (int64_t)t * ld);
-    float y[EPL];
-    float ss = 0.0f;
+  for (int sl = w; sl < 3 * H; sl += kWaves) {
+    const int which = sl / H, h = sl % H;
+    const T* src = (which == 0 ? q : (which == 1 ? k : v)) + (int64_t)b * Tn * ld + h * kD +
+                   sub * EPL;
+    T* dst = (which == 0 ? q_out : (which == 1 ? k_out : v_out)) +
+             ((int64_t)b * H + h) * Tn * kD + sub * EPL;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      y[e] = ok ? to_f(xin[e]) : 0.0f;
-      ss = __builtin_fmaf(y[e], y[e], ss);
-    }
-    if (NORM) {
-      ss = group_sum<LPR>(ss);
-      const float tau = rsq(ss * (1.0f / kD) + eps);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) y[e] = round_to<T>((y[e] * tau) * g[e]);
-    }
-    VT out;
-    if (ROT) {
-      const int tc = ok ? t : 0;
+    for (int i = 0; i < kBlockTokens; i += RPW) {
+      const int t = t0 + i + rw;
+      const bool ok = t < Tn;
+      VT xin;
+      if (ok) xin = *reinterpret_cast<const VT*>(src + (int64_t)t * ld);
+      if (which == 2) {
+        if (ok) *reinterpret_cast<VT*>(dst + (int64_t)t * kD) = xin;
+        continue;
+      }
+      float y[EPL];
+      float ss = 0.0f;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
-        const float p = __shfl_xor(y[e], HALF, 64);
-        const float c = round_to<T>(cosb[(int64_t)tc * (kD / 2) + j0 + e]);
-        const float s = round_to<T>(sinb[(int64_t)tc * (kD / 2) + j0 + e]);
-        // first half: x1 c - x2 s; second half: x1 s + x2 c
-        const float r = first ? round_to<T>(y[e] * c) - round_to<T>(p * s)
-                              : round_to<T>(p * s) + round_to<T>(y[e] * c);
-        out[e] = from_f<T>(r);
+        y[e] = ok ? to_f(xin[e]) : 0.0f;
+        ss = __builtin_fmaf(y[e], y[e], ss);
       }
-    } else {
+      if (NORM) {
+        ss = group_sum<LPR>(ss);
+        const float tau = rsq(ss * (1.0f / kD) + eps);
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) out[e] = from_f<T>(y[e]);
+        for (int e = 0; e < EPL; ++e)
+          y[e] = round_to<T>((y[e] * tau) * (which == 0 ? gq[e] : gk[e]));
+      }
+      VT out;
+      if (ROT) {
+        const int tc = ok ? t : 0;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          const float p = __shfl_xor(y[e], HALF, 64);
+          const float c = round_to<T>(cosb[(int64_t)tc * (kD / 2) + j0 + e]);
+          const float s = round_to<T>(sinb[(int64_t)tc * (kD / 2) + j0 + e]);
+          // first half: x1 c - x2 s; second half: x1 s + x2 c
+          const float r = first ? round_to<T>(y[e] * c) - round_to<T>(p * s)
+                                : round_to<T>(p * s) + round_to<T>(y[e] * c);
+          out[e] = from_f<T>(r);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) out[e] = from_f<T>(y[e]);
+      }
+      if (ok) *reinterpret_cast<VT*>(dst + (int64_t)t * kD) = out;
     }
-    if (ok) *reinterpret_cast<VT*>(dst + (int64_t)t * kD) = out;
   }
 }
 
@@ -133,141 +118,154 @@ __global__ __launch_bounds__(kThreads) void prologue_fwd_kernel(
 // and sums), then the RMS-norm input VJP
 //   dx = tau g dy - x tau^3 sum(dy g x) / D,   dgain += dy x tau,
 // written into the projection-gradient rows; v's gradient is copied back.
+// Same workgroup map as the forward; partial: [workgroup][q, k][D].
 template <typename T, bool NORM, bool ROT>
 __global__ __launch_bounds__(kThreads) void prologue_bwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, int64_t ld, const float* __restrict__ q_gain,
     const float* __restrict__ k_gain, const float* __restrict__ cosb,
     const float* __restrict__ sinb, const T* __restrict__ dq_out, const T* __restrict__ dk_out,
     const T* __restrict__ dv_out, T* __restrict__ dq, T* __restrict__ dk, T* __restrict__ dv,
-    float* __restrict__ partial, int B, int Tn, int H, int nseg, float eps) {
+    float* __restrict__ partial, int Tn, int H, int ntb, float eps) {
   typedef typename Vec<T>::type VT;
   constexpr int EPL = Vec<T>::n;
   constexpr int LPR = kD / EPL;
   constexpr int RPW = 64 / LPR;
   constexpr int HALF = LPR / 2;
-  const Seg sg = seg_of(B, H, nseg);
+  const int b = blockIdx.x / ntb, t0 = (blockIdx.x % ntb) * kBlockTokens;
   const int lane = threadIdx.x & 63, sub = lane % LPR, rw = lane / LPR, w = threadIdx.x >> 6;
-  const int64_t head_off = ((int64_t)sg.b * H + sg.h) * Tn * kD + sub * EPL;
-  const int64_t row_off = (int64_t)sg.b * Tn * ld + sg.h * kD + sub * EPL;
-  if (sg.which == 2) {
-    for (int i = 0; i < kWaveTokens; i += RPW) {
-      const int t = sg.t0 + i + rw;
-      if (t < Tn)
-        *reinterpret_cast<VT*>(dv + row_off + (int64_t)t * ld) =
-            *reinterpret_cast<const VT*>(dv_out + head_off + (int64_t)t * kD);
-    }
-    return;
-  }
-  const T* x = (sg.which == 0 ? q : k) + row_off;
-  const T* dout = (sg.which == 0 ? dq_out : dk_out) + head_off;
-  T* dx = (sg.which == 0 ? dq : dk) + row_off;
-  const float* gain = sg.which == 0 ? q_gain : k_gain;
-  float g[EPL], dg[EPL];
+  float gq[EPL], gk[EPL], dgq[EPL], dgk[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
-    g[e] = NORM ? gain[sub * EPL + e] : 1.0f;
-    dg[e] = 0.0f;
+    gq[e] = NORM ? q_gain[sub * EPL + e] : 1.0f;
+    gk[e] = NORM ? k_gain[sub * EPL + e] : 1.0f;
+    dgq[e] = 0.0f;
+    dgk[e] = 0.0f;
   }
   const int j0 = (sub % HALF) * EPL;
   const bool first = sub < HALF;
-#pragma unroll 2
-  for (int i = 0; i < kWaveTokens; i += RPW) {
-    const int t = sg.t0 + i + rw;
-    const bool ok = t < Tn;
-    VT din, xin;
-    if (ok) {
-      din = *reinterpret_cast<const VT*>(dout + (int64_t)t * kD);
-      if (NORM) xin = *reinterpret_cast<const VT*>(x + (int64_t)t * ld);
-    }
-    float dy[EPL];
+  for (int sl = w; sl < 3 * H; sl += kWaves) {
+    const int which = sl / H, h = sl % H;
+    const int64_t head_off = ((int64_t)b * H + h) * Tn * kD + sub * EPL;
+    const int64_t row_off = (int64_t)b * Tn * ld + h * kD + sub * EPL;
+    const T* dout = (which == 0 ? dq_out : (which == 1 ? dk_out : dv_out)) + head_off;
+    T* dx = (which == 0 ? dq : (which == 1 ? dk : dv)) + row_off;
+    const T* x = (which == 0 ? q : k) + row_off;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) dy[e] = ok ? to_f(din[e]) : 0.0f;
-    if (ROT) {
-      const int tc = ok ? t : 0;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const float p = __shfl_xor(dy[e], HALF, 64);
-        const float c = round_to<T>(cosb[(int64_t)tc * (kD / 2) + j0 + e]);
-        const float s = round_to<T>(sinb[(int64_t)tc * (kD / 2) + j0 + e]);
-        // dx1 = d1 c + d2 s; dx2 = d2 c - d1 s
-        dy[e] = first ? round_to<T>(round_to<T>(dy[e] * c) + round_to<T>(p * s))
-                      : round_to<T>(round_to<T>(dy[e] * c) - round_to<T>(p * s));
+    for (int i = 0; i < kBlockTokens; i += RPW) {
+      const int t = t0 + i + rw;
+      const bool ok = t < Tn;
+      VT din, xin;
+      if (ok) {
+        din = *reinterpret_cast<const VT*>(dout + (int64_t)t * kD);
+        if (NORM && which != 2) xin = *reinterpret_cast<const VT*>(x + (int64_t)t * ld);
       }
-    }
-    VT out;
-    if (NORM) {
-      float xs[EPL];
-      float ss = 0.0f, dot = 0.0f;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        xs[e] = ok ? to_f(xin[e]) : 0.0f;
-        ss = __builtin_fmaf(xs[e], xs[e], ss);
-        dot = __builtin_fmaf(dy[e] * g[e], xs[e], dot);
+      if (which == 2) {
+        if (ok) *reinterpret_cast<VT*>(dx + (int64_t)t * ld) = din;
+        continue;
       }
-      ss = group_sum<LPR>(ss);
-      dot = group_sum<LPR>(dot);
-      const float tau = rsq(ss * (1.0f / kD) + eps);
-      const float cf = tau * tau * tau * dot * (1.0f / kD);
+      float dy[EPL];
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        out[e] = from_f<T>(tau * g[e] * dy[e] - cf * xs[e]);
-        dg[e] = __builtin_fmaf(dy[e], xs[e] * tau, dg[e]);
+      for (int e = 0; e < EPL; ++e) dy[e] = ok ? to_f(din[e]) : 0.0f;
+      if (ROT) {
+        const int tc = ok ? t : 0;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          const float p = __shfl_xor(dy[e], HALF, 64);
+          const float c = round_to<T>(cosb[(int64_t)tc * (kD / 2) + j0 + e]);
+          const float s = round_to<T>(sinb[(int64_t)tc * (kD / 2) + j0 + e]);
+          // dx1 = d1 c + d2 s; dx2 = d2 c - d1 s
+          dy[e] = first ? round_to<T>(round_to<T>(dy[e] * c) + round_to<T>(p * s))
+                        : round_to<T>(round_to<T>(dy[e] * c) - round_to<T>(p * s));
+        }
       }
-    } else {
+      VT out;
+      if (NORM) {
+        float xs[EPL], g[EPL];
+        float ss = 0.0f, dot = 0.0f;
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) out[e] = from_f<T>(dy[e]);
+        for (int e = 0; e < EPL; ++e) {
+          g[e] = which == 0 ? gq[e] : gk[e];
+          xs[e] = ok ? to_f(xin[e]) : 0.0f;
+          ss = __builtin_fmaf(xs[e], xs[e], ss);
+          dot = __builtin_fmaf(dy[e] * g[e], xs[e], dot);
+        }
+        ss = group_sum<LPR>(ss);
+        dot = group_sum<LPR>(dot);
+        const float tau = rsq(ss * (1.0f / kD) + eps);
+        const float cf = tau * tau * tau * dot * (1.0f / kD);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          out[e] = from_f<T>(tau * g[e] * dy[e] - cf * xs[e]);
+          if (which == 0)
+            dgq[e] = __builtin_fmaf(dy[e], xs[e] * tau, dgq[e]);
+          else
+            dgk[e] = __builtin_fmaf(dy[e], xs[e] * tau, dgk[e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) out[e] = from_f<T>(dy[e]);
+      }
+      if (ok) *reinterpret_cast<VT*>(dx + (int64_t)t * ld) = out;
     }
-    if (ok) *reinterpret_cast<VT*>(dx + (int64_t)t * ld) = out;
   }
   if (!NORM) return;
   // Workgroup share of dgain: rows of the wave by xor-shuffles, then the
-  // four waves in order through LDS; one partial row per workgroup.
-  __shared__ float red[kThreads / 64][kD];
+  // four waves in order through LDS.
+  __shared__ float red[kWaves][2][kD];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
-    float s = dg[e];
+    float a = dgq[e], c = dgk[e];
 #pragma unroll
-    for (int m = LPR; m < 64; m <<= 1) s += __shfl_xor(s, m, 64);
-    dg[e] = s;
+    for (int m = LPR; m < 64; m <<= 1) {
+      a += __shfl_xor(a, m, 64);
+      c += __shfl_xor(c, m, 64);
+    }
+    dgq[e] = a;
+    dgk[e] = c;
   }
   if (rw == 0) {
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) red[w][sub * EPL + e] = dg[e];
+    for (int e = 0; e < EPL; ++e) {
+      red[w][0][sub * EPL + e] = dgq[e];
+      red[w][1][sub * EPL + e] = dgk[e];
+    }
   }
   __syncthreads();
-  if (threadIdx.x < kD) {
+  if (threadIdx.x < 2 * kD) {
+    const int which = threadIdx.x / kD, col = threadIdx.x % kD;
     float s = 0.0f;
 #pragma unroll
-    for (int ww = 0; ww < kThreads / 64; ++ww) s += red[ww][threadIdx.x];
-    // partial rows of q first, then k: [which][b][h][seg]
-    partial[(int64_t)blockIdx.x * kD + threadIdx.x] = s;
+    for (int ww = 0; ww < kWaves; ++ww) s += red[ww][which][col];
+    partial[((int64_t)blockIdx.x * 2 + which) * kD + col] = s;
   }
 }
 
-// dgain of q (block 0) and k (block 1): the workgroup partials of that
-// tensor, 64 columns x 4 interleaved slices, combined in slice order.
-__global__ __launch_bounds__(256) void prologue_gain_finish(const float* __restrict__ partial,
-                                                            int nparts, float* __restrict__ dq_gain,
-                                                            float* __restrict__ dk_gain) {
-  __shared__ float red[4][kD];
+// dgain of q (block 0) and k (block 1) from the workgroup partials: 64
+// columns x 16 interleaved slices of the workgroups, combined in slice order.
+__global__ __launch_bounds__(1024) void prologue_gain_finish(const float* __restrict__ partial,
+                                                             int nparts, float* __restrict__ dq_gain,
+                                                             float* __restrict__ dk_gain) {
+  __shared__ float red[16][kD];
   const int col = threadIdx.x & 63, slice = threadIdx.x >> 6;
-  const float* p = partial + (int64_t)blockIdx.x * nparts * kD;
+  const int which = blockIdx.x;
   float s0 = 0.0f, s1 = 0.0f;
   int r = slice;
-  for (; r + 4 < nparts; r += 8) {
-    s0 += p[(int64_t)r * kD + col];
-    s1 += p[(int64_t)(r + 4) * kD + col];
+  for (; r + 16 < nparts; r += 32) {
+    s0 += partial[((int64_t)r * 2 + which) * kD + col];
+    s1 += partial[((int64_t)(r + 16) * 2 + which) * kD + col];
   }
-  if (r < nparts) s0 += p[(int64_t)r * kD + col];
+  if (r < nparts) s0 += partial[((int64_t)r * 2 + which) * kD + col];
   red[slice][col] = s0 + s1;
   __syncthreads();
   if (slice == 0) {
-    const float s = (red[0][col] + red[1][col]) + (red[2][col] + red[3][col]);
-    (blockIdx.x == 0 ? dq_gain : dk_gain)[col] = s;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += red[i][col];
+    (which == 0 ? dq_gain : dk_gain)[col] = s;
   }
 }
 
-int nseg_of(int T) { return (T + kSegTokens - 1) / kSegTokens; }
+int ntb_of(int T) { return (T + kBlockTokens - 1) / kBlockTokens; }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -295,12 +293,12 @@ int32_t check_prologue(const void* q, const void* k, const void* v, int64_t ld,
 template <typename T>
 void launch_fwd(bool norm, bool rot, dim3 grid, hipStream_t s, const void* q, const void* k,
                 const void* v, int64_t ld, const float* qg, const float* kg, const float* cb,
-                const float* sb, void* qo, void* ko, void* vo, int B, int Tn, int H, int nseg,
+                const float* sb, void* qo, void* ko, void* vo, int Tn, int H, int ntb,
                 float eps) {
 #define ALGX_PRO_FWD(N, R)                                                                  \
   prologue_fwd_kernel<T, N, R><<<grid, kThreads, 0, s>>>(                                   \
-      (const T*)q, (const T*)k, (const T*)v, ld, qg, kg, cb, sb, (T*)qo, (T*)ko, (T*)vo, B, Tn, \
-      H, nseg, eps)
+      (const T*)q, (const T*)k, (const T*)v, ld, qg, kg, cb, sb, (T*)qo, (T*)ko, (T*)vo, Tn, H, \
+      ntb, eps)
   if (norm && rot) ALGX_PRO_FWD(true, true);
   else if (norm) ALGX_PRO_FWD(true, false);
   else if (rot) ALGX_PRO_FWD(false, true);
@@ -312,11 +310,11 @@ template <typename T>
 void launch_bwd(bool norm, bool rot, dim3 grid, hipStream_t s, const void* q, const void* k,
                 int64_t ld, const float* qg, const float* kg, const float* cb, const float* sb,
                 const void* dqo, const void* dko, const void* dvo, void* dq, void* dk, void* dv,
-                float* partial, int B, int Tn, int H, int nseg, float eps) {
+                float* partial, int Tn, int H, int ntb, float eps) {
 #define ALGX_PRO_BWD(N, R)                                                                   \
   prologue_bwd_kernel<T, N, R><<<grid, kThreads, 0, s>>>(                                    \
       (const T*)q, (const T*)k, ld, qg, kg, cb, sb, (const T*)dqo, (const T*)dko,            \
-      (const T*)dvo, (T*)dq, (T*)dk, (T*)dv, partial, B, Tn, H, nseg, eps)
+      (const T*)dvo, (T*)dq, (T*)dk, (T*)dv, partial, Tn, H, ntb, eps)
   if (norm && rot) ALGX_PRO_BWD(true, true);
   else if (norm) ALGX_PRO_BWD(true, false);
   else if (rot) ALGX_PRO_BWD(false, true);
@@ -342,16 +340,16 @@ extern "C" int32_t algx_qk_prologue_fwd(const void* q, const void* k, const void
     return fail("qk_prologue: null output");
   if (!aligned16(q_out) || !aligned16(k_out) || !aligned16(v_out))
     return fail("qk_prologue: operands must be 16-byte aligned");
-  const int nseg = nseg_of(T);
-  const dim3 grid((unsigned)(3 * (int64_t)B * H * nseg));
+  const int ntb = ntb_of(T);
+  const dim3 grid((unsigned)((int64_t)B * ntb));
   hipStream_t s = (hipStream_t)stream;
   const bool norm = q_gain != nullptr, rot = cos_t != nullptr;
   if (dtype == ALGX_BF16)
     launch_fwd<bf16>(norm, rot, grid, s, q, k, v, ld, q_gain, k_gain, cos_t, sin_t, q_out, k_out,
-                     v_out, B, T, H, nseg, eps);
+                     v_out, T, H, ntb, eps);
   else
     launch_fwd<float>(norm, rot, grid, s, q, k, v, ld, q_gain, k_gain, cos_t, sin_t, q_out, k_out,
-                      v_out, B, T, H, nseg, eps);
+                      v_out, T, H, ntb, eps);
   return check_launch("qk_prologue_fwd");
 }
 
@@ -360,7 +358,7 @@ extern "C" int64_t algx_qk_prologue_bwd_workspace_bytes(int32_t B, int32_t T, in
   (void)D;
   (void)dtype;
   if (B <= 0 || T <= 0 || H <= 0) return 0;
-  return 2 * (int64_t)B * H * nseg_of(T) * kD * (int64_t)sizeof(float);
+  return 2 * (int64_t)B * ntb_of(T) * kD * (int64_t)sizeof(float);
 }
 
 extern "C" int32_t algx_qk_prologue_bwd(const void* q, const void* k, const float* q_gain,
@@ -390,17 +388,17 @@ extern "C" int32_t algx_qk_prologue_bwd(const void* q, const void* k, const floa
       !aligned16(dk) || !aligned16(dv))
     return fail("qk_prologue: operands must be 16-byte aligned");
   if (norm && workspace == nullptr) return fail("qk_prologue: null workspace");
-  const int nseg = nseg_of(T);
-  const dim3 grid((unsigned)(3 * (int64_t)B * H * nseg));
+  const int ntb = ntb_of(T);
+  const dim3 grid((unsigned)((int64_t)B * ntb));
   float* partial = (float*)workspace;
   if (dtype == ALGX_BF16)
     launch_bwd<bf16>(norm, rot, grid, s, q, k, ld, q_gain, k_gain, cos_t, sin_t, dq_out, dk_out,
-                     dv_out, dq, dk, dv, partial, B, T, H, nseg, eps);
+                     dv_out, dq, dk, dv, partial, T, H, ntb, eps);
   else
     launch_bwd<float>(norm, rot, grid, s, q, k, ld, q_gain, k_gain, cos_t, sin_t, dq_out, dk_out,
-                      dv_out, dq, dk, dv, partial, B, T, H, nseg, eps);
+                      dv_out, dq, dk, dv, partial, T, H, ntb, eps);
   if (int32_t rc = check_launch("qk_prologue_bwd")) return rc;
   if (!norm) return 0;
-  prologue_gain_finish<<<2, 256, 0, s>>>(partial, B * H * nseg, dq_gain, dk_gain);
+  prologue_gain_finish<<<2, 1024, 0, s>>>(partial, B * ntb, dq_gain, dk_gain);
   return check_launch("qk_prologue_gain_finish");
 }

@@ -190,6 +190,18 @@ int32_t algx_alu_glu_fwd(const void* gate, const void* up, void* out, int64_t n,
 int32_t algx_alu_glu_bwd(const void* gate, const void* up, const void* dout, void* dgate,
                          void* dup, int64_t n, int32_t dtype, float beta, void* stream);
 
+/* The feed-forward product on the packed projection gu = [gate | up]
+ * (rows x 2 cols, the output of one GEMM against [w_g | w_u], model.py:184-191):
+ * y (rows x cols) = cast(gate * act(up)) with act = ALGX_GLU_ALU (alu, beta, as
+ * algx_alu_glu_fwd) or ALGX_GLU_SILU (x * cast(sigmoid(x)), standard.py:12-13).
+ * The backward writes dgu = [dgate | dup] (rows x 2 cols). cols a multiple of 8
+ * (bf16) or 4 (f32). */
+enum { ALGX_GLU_ALU = 0, ALGX_GLU_SILU = 1 };
+int32_t algx_glu_packed_fwd(const void* gu, void* y, int64_t rows, int32_t cols, int32_t act,
+                            int32_t dtype, float beta, void* stream);
+int32_t algx_glu_packed_bwd(const void* gu, const void* dy, void* dgu, int64_t rows, int32_t cols,
+                            int32_t act, int32_t dtype, float beta, void* stream);
+
 /* ------------------------------------------------------ attention prologue
  * The model block's step from projections to attention inputs
  * (src/algebraic/model.py:166-174) in one pass: q, k, v are rows of the

@@ -12,6 +12,8 @@ dtype:
   alu(up)`` of model.py:186-191 and the autodiff VJP of that product, which
   rounds ``dout * gate`` and ``dout * act`` to the storage dtype as the
   unfused bf16 multiplies do.
+* ``swiglu`` / ``swiglu_vjp`` -- the standard preset's ``gate * silu(up)``
+  (standard.py:12-13), rounding the sigmoid and each product.
 
 Pinned in tests/test_oracle_elementwise.py against the closed form and
 finite differences (the reference's own test_components.py:71-78 grid),
@@ -91,3 +93,23 @@ def alu_glu_vjp(gate, up, dout, beta, dtype):
     dgate = cast(dout * act, dtype)
     gact = cast(dout * np.asarray(gate, F64), dtype)
     return dgate, alu_vjp(up, gact, beta, dtype)
+
+
+def swiglu(gate, up, dtype):
+    """gate * silu(up), silu(x) = x * sigmoid(x) with sigmoid and every product
+    rounded to the storage dtype (standard.py:12-13, model.py:186-188)."""
+    up = np.asarray(up, F64)
+    sg = cast(1.0 / (1.0 + np.exp(-up)), dtype)
+    act = cast(up * sg, dtype)
+    return cast(np.asarray(gate, F64) * act, dtype)
+
+
+def swiglu_vjp(gate, up, dout, dtype):
+    """(dgate, dup): dgate = cast(dout * act), dup = cast(cast(dout * gate) *
+    silu'(up)) with silu' = s + x s (1 - s) unrounded."""
+    up = np.asarray(up, F64)
+    s = 1.0 / (1.0 + np.exp(-up))
+    act = cast(up * cast(s, dtype), dtype)
+    dout = np.asarray(dout, F64)
+    gact = cast(dout * np.asarray(gate, F64), dtype)
+    return cast(dout * act, dtype), cast(gact * (s + up * s * (1.0 - s)), dtype)

@@ -169,3 +169,43 @@ def test_alu_glu_equals_unfused_ops():
     assert torch.equal(fused, unfused)
     assert torch.equal(g1.grad, g2.grad)
     assert torch.equal(u1.grad, u2.grad)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_glu_packed_alu_equals_alu_glu(dtype):
+    """[gate | up] from one GEMM: the packed kernel gives alu_glu's outputs
+    and gradients bit for bit, the gradient packed as [dgate | dup]."""
+    from algebraic_amd.algebraic import glu_packed
+    rng = np.random.default_rng(21)
+    rows, f = 3000, 2688
+    gu = _randn(rng, (rows, 2 * f), dtype, 2.0).to(DEV)
+    dout = _randn(rng, (rows, f), dtype).to(DEV)
+    a = gu.clone().requires_grad_(True)
+    ya = glu_packed(a, "alu", 0.5)
+    ya.backward(dout)
+    gate = gu[:, :f].contiguous().requires_grad_(True)
+    up = gu[:, f:].contiguous().requires_grad_(True)
+    yb = alu_glu(gate, up, 0.5)
+    yb.backward(dout)
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yb)
+    assert torch.equal(a.grad[:, :f], gate.grad) and torch.equal(a.grad[:, f:], up.grad)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("rows,f", [(37, 96), (2048, 2688)])
+def test_glu_packed_silu_matches_oracle(dtype, rows, f):
+    """The standard preset's SwiGLU on the packed projection (standard.py:12-13)."""
+    from algebraic_amd.algebraic import glu_packed
+    rng = np.random.default_rng(rows + f)
+    gu = _randn(rng, (rows, 2 * f), dtype, 3.0)
+    dout = _randn(rng, (rows, f), dtype)
+    t = gu.to(DEV).requires_grad_(True)
+    y = glu_packed(t, "silu")
+    y.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    g, u, d = to_np(gu[:, :f]), to_np(gu[:, f:]), to_np(dout)
+    _check(dtype)(y, OE.swiglu(g, u, dtype), what="y")
+    want_dg, want_du = OE.swiglu_vjp(g, u, d, dtype)
+    _check(dtype)(t.grad[:, :f], want_dg, what="dgate")
+    _check(dtype)(t.grad[:, f:], want_du, what="dup")

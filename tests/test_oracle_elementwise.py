@@ -146,3 +146,19 @@ def test_rms_norm_invariants():
     # dx of a scale-invariant map is orthogonal to x (eps -> 0): sum(dx * x) = 0
     dx, _ = OE.rms_norm_vjp(x, None, rng.standard_normal(x.shape), 1e-300, "f64")
     np.testing.assert_allclose(np.sum(dx * x, -1), 0.0, atol=1e-10)
+
+
+def test_swiglu_oracle_matches_autograd():
+    """In float64 (no roundings) the SwiGLU oracle and its VJP are torch
+    autograd of gate * up * sigmoid(up)."""
+    rng = np.random.default_rng(12)
+    gate, up, dout = (rng.standard_normal(2048) * 3 for _ in range(3))
+    tg = torch.tensor(gate, requires_grad=True)
+    tu = torch.tensor(up, requires_grad=True)
+    out = tg * tu * torch.sigmoid(tu)
+    (out * torch.tensor(dout)).sum().backward()
+    np.testing.assert_allclose(OE.swiglu(gate, up, "f64"), out.detach().numpy(), rtol=1e-12,
+                               atol=1e-14)
+    dg, du = OE.swiglu_vjp(gate, up, dout, "f64")
+    np.testing.assert_allclose(dg, tg.grad.numpy(), rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(du, tu.grad.numpy(), rtol=1e-10, atol=1e-13)
