@@ -11,9 +11,9 @@
 //
 // D = 64. A row (b, t, h) is 128 bytes in bf16: 8 lanes of 16 bytes (16
 // lanes in f32). The rotate-half partner of a lane's elements sits in lane
-// ^ (lanes per row / 2), one xor-shuffle away. A workgroup owns 16 tokens of
+// ^ (lanes per row / 2), one xor-shuffle away. A workgroup owns 8 tokens of
 // one sequence and every head slice of their q, k and v rows, so it reads
-// whole projection rows and writes 2 KB runs of the (B, H, T, D) outputs.
+// whole projection rows and writes 1 KB runs of the (B, H, T, D) outputs.
 // The gain gradients are reduced per workgroup and finished per column in a
 // fixed order.
 #include "common.h"
@@ -25,7 +25,7 @@ namespace {
 constexpr int kD = 64;
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kBlockTokens = 16;
+constexpr int kBlockTokens = 8;
 
 template <typename T> struct Vec;
 template <> struct Vec<bf16> { typedef bf16x8 type; static constexpr int n = 8; };
@@ -37,9 +37,9 @@ template <int LPR> __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// A workgroup owns 16 consecutive tokens of one sequence and all 3 H head
+// A workgroup owns 8 consecutive tokens of one sequence and all 3 H head
 // slices of their projection rows (q heads, then k, then v): it reads whole
-// rows, and each (slice, 16 tokens) it writes is one contiguous 2 KB run of
+// rows, and each (slice, 8 tokens) it writes is one contiguous 1 KB run of
 // the (B, H, T, D) output. Wave w takes slices w, w + 4, ...
 template <typename T, bool NORM, bool ROT>
 __global__ __launch_bounds__(kThreads) void prologue_fwd_kernel(
@@ -95,11 +95,20 @@ __global__ __launch_bounds__(kThreads) void prologue_fwd_kernel(
       VT out;
       if (ROT) {
         const int tc = ok ? t : 0;
+        // the lane's EPL table entries as 16-byte loads (j0 is a multiple of EPL)
+        float cv[EPL], sv[EPL];
+#pragma unroll
+        for (int q4 = 0; q4 < EPL; q4 += 4) {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(cosb + (int64_t)tc * (kD / 2) + j0 + q4);
+          const f32x4 bb = *reinterpret_cast<const f32x4*>(sinb + (int64_t)tc * (kD / 2) + j0 + q4);
+#pragma unroll
+          for (int z = 0; z < 4; ++z) { cv[q4 + z] = a[z]; sv[q4 + z] = bb[z]; }
+        }
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
           const float p = __shfl_xor(y[e], HALF, 64);
-          const float c = round_to<T>(cosb[(int64_t)tc * (kD / 2) + j0 + e]);
-          const float s = round_to<T>(sinb[(int64_t)tc * (kD / 2) + j0 + e]);
+          const float c = round_to<T>(cv[e]);
+          const float s = round_to<T>(sv[e]);
           // first half: x1 c - x2 s; second half: x1 s + x2 c
           const float r = first ? round_to<T>(y[e] * c) - round_to<T>(p * s)
                                 : round_to<T>(p * s) + round_to<T>(y[e] * c);
@@ -168,11 +177,20 @@ __global__ __launch_bounds__(kThreads) void prologue_bwd_kernel(
       for (int e = 0; e < EPL; ++e) dy[e] = ok ? to_f(din[e]) : 0.0f;
       if (ROT) {
         const int tc = ok ? t : 0;
+        // the lane's EPL table entries as 16-byte loads (j0 is a multiple of EPL)
+        float cv[EPL], sv[EPL];
+#pragma unroll
+        for (int q4 = 0; q4 < EPL; q4 += 4) {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(cosb + (int64_t)tc * (kD / 2) + j0 + q4);
+          const f32x4 bb = *reinterpret_cast<const f32x4*>(sinb + (int64_t)tc * (kD / 2) + j0 + q4);
+#pragma unroll
+          for (int z = 0; z < 4; ++z) { cv[q4 + z] = a[z]; sv[q4 + z] = bb[z]; }
+        }
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
           const float p = __shfl_xor(dy[e], HALF, 64);
-          const float c = round_to<T>(cosb[(int64_t)tc * (kD / 2) + j0 + e]);
-          const float s = round_to<T>(sinb[(int64_t)tc * (kD / 2) + j0 + e]);
+          const float c = round_to<T>(cv[e]);
+          const float s = round_to<T>(sv[e]);
           // dx1 = d1 c + d2 s; dx2 = d2 c - d1 s
           dy[e] = first ? round_to<T>(round_to<T>(dy[e] * c) + round_to<T>(p * s))
                         : round_to<T>(round_to<T>(dy[e] * c) - round_to<T>(p * s));

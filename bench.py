@@ -251,6 +251,19 @@ def bench_model(preset, steps, warmup, dev, B=8, T=2048, V=50304):
     (no optimiser update)."""
     import torch
     from algebraic_amd import config, model
+    # Plain library GEMMs: torch's TunableOp picks, per projection shape, the
+    # fastest hipBLASLt or rocBLAS solution recorded for this ROCm/torch build
+    # (selection only: no tuning runs here; unknown shapes keep the default).
+    table = os.path.join(os.path.dirname(os.path.abspath(__file__)), "algebraic-extra_amd",
+                         "algebraic_amd", "gemm_tuning_gfx950.csv")
+    if os.path.exists(table):
+        import tempfile
+        torch.cuda.tunable.enable(True)
+        torch.cuda.tunable.tuning_enable(False)
+        # results are read from the table; anything written back goes to /tmp
+        torch.cuda.tunable.set_filename(os.path.join(tempfile.gettempdir(),
+                                                     f"algx_tunableop_{os.getpid()}.csv"))
+        torch.cuda.tunable.read_file(table)
     cfg = config.build(preset, "350m", vocab_size=V, seq_len=T, attn_impl="flash",
                        head_impl="fused")
     params = model.init_params(cfg, seed=0, device=dev)
@@ -273,6 +286,8 @@ def bench_model(preset, steps, warmup, dev, B=8, T=2048, V=50304):
            "tflops": fpt * B * T / dt / 1e12, "flops_per_token": fpt,
            "frac": fpt * B * T / dt / 1e12 / PEAK_BF16_TFLOPS,
            "params": model.count_params(params)}
+    out["gemm_selection"] = "tunableop table" if torch.cuda.tunable.is_enabled() else "default"
+    torch.cuda.tunable.enable(False)
     del params, leaves
     torch.cuda.empty_cache()
     return out
