@@ -244,11 +244,13 @@ def model_flops_per_token(cfg, T):
     return 6 * dense + 3.5 * L * 2 * H * T * D
 
 
-def bench_model(preset, steps, warmup, dev, B=8, T=2048, V=50304):
+def bench_model(preset, steps, warmup, dev, B=8, T=2048, V=50304, remat=True):
     """one forward + backward of the 350M preset (d 1024, 24 layers,
     16 heads of 64, d_ff 2688, V 50304) on B x T random tokens, random-init
-    weights, bf16, rematerialised blocks; parameter gradients are produced
-    (no optimiser update)."""
+    weights, bf16; parameter gradients are produced (no optimiser update).
+    remat=True recomputes each block in the backward as the reference's
+    default LMConfig does; remat=False keeps the activations (they fit in HBM
+    at this size many times over)."""
     import torch
     from algebraic_amd import config, model
     # Plain library GEMMs: torch's TunableOp picks, per projection shape, the
@@ -265,7 +267,7 @@ def bench_model(preset, steps, warmup, dev, B=8, T=2048, V=50304):
                                                      f"algx_tunableop_{os.getpid()}.csv"))
         torch.cuda.tunable.read_file(table)
     cfg = config.build(preset, "350m", vocab_size=V, seq_len=T, attn_impl="flash",
-                       head_impl="fused")
+                       head_impl="fused", remat=remat)
     params = model.init_params(cfg, seed=0, device=dev)
     leaves = list(model._leaves(params))
     gen = torch.Generator(device=dev).manual_seed(5)
@@ -279,9 +281,12 @@ def bench_model(preset, steps, warmup, dev, B=8, T=2048, V=50304):
         obj, _ = model.train_objective(params, x, y, cfg, tables)
         obj.backward()
 
-    dt = time_steps(step, steps, warmup)
     fpt = model_flops_per_token(cfg, T)
-    out = {"workload": f"configs[4] {preset} 350M fwd+bwd, B={B}, T={T}, V={V}, bf16, remat",
+    torch.cuda.reset_peak_memory_stats()
+    dt = time_steps(step, steps, warmup)
+    out = {"workload": f"configs[4] {preset} 350M fwd+bwd, B={B}, T={T}, V={V}, bf16, "
+                       f"{'remat' if remat else 'no remat'}",
+           "peak_hbm_gb": torch.cuda.max_memory_allocated() / 1e9,
            "ms_per_step": dt * 1e3, "tokens_per_s": B * T / dt,
            "tflops": fpt * B * T / dt / 1e12, "flops_per_token": fpt,
            "frac": fpt * B * T / dt / 1e12 / PEAK_BF16_TFLOPS,
@@ -353,10 +358,11 @@ def main():
               flush=True)
         return
     if args.model_only:
-        for preset in ("algebraic", "standard"):
+        for preset, remat in (("algebraic", False), ("standard", False), ("algebraic", True),
+                              ("standard", True)):
             print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
-                              for k, v in bench_model(preset, args.steps, args.warmup,
-                                                      dev).items()}), flush=True)
+                              for k, v in bench_model(preset, args.steps, args.warmup, dev,
+                                                      remat=remat).items()}), flush=True)
         return
     if args.elementwise_only:
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
@@ -422,10 +428,10 @@ def main():
             "elementwise": {k: (round(v, 4) if isinstance(v, float) else v)
                             for k, v in bench_elementwise(20, 3, dev).items()},
         }
-        for preset in ("algebraic", "standard"):
-            line["secondary"][f"model_350m_{preset}"] = {
+        for preset, remat in (("algebraic", False), ("standard", False), ("algebraic", True)):
+            line["secondary"][f"model_350m_{preset}{'_remat' if remat else ''}"] = {
                 k: (round(v, 4) if isinstance(v, float) else v)
-                for k, v in bench_model(preset, 5, 2, dev).items()}
+                for k, v in bench_model(preset, 5, 2, dev, remat=remat).items()}
     if not args.no_cpu:
         line["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                 for k, v in cpu_baseline(B, H, T, D).items()}
