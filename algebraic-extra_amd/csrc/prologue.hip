@@ -258,29 +258,29 @@ __global__ __launch_bounds__(kThreads) void prologue_bwd_kernel(
   }
 }
 
-// dgain of q (block 0) and k (block 1) from the workgroup partials: 64
-// columns x 16 interleaved slices of the workgroups, combined in slice order.
-__global__ __launch_bounds__(1024) void prologue_gain_finish(const float* __restrict__ partial,
-                                                             int nparts, float* __restrict__ dq_gain,
-                                                             float* __restrict__ dk_gain) {
-  __shared__ float red[16][kD];
-  const int col = threadIdx.x & 63, slice = threadIdx.x >> 6;
-  const int which = blockIdx.x;
+// dgain of q and k from the workgroup partials: one workgroup per (tensor,
+// column), each thread summing a strided slice of the partial rows with
+// independent loads in flight, then a fixed-order tree in LDS.
+__global__ __launch_bounds__(256) void prologue_gain_finish(const float* __restrict__ partial,
+                                                            int nparts, float* __restrict__ dq_gain,
+                                                            float* __restrict__ dk_gain) {
+  __shared__ float red[256];
+  const int which = blockIdx.x / kD, col = blockIdx.x % kD;
   float s0 = 0.0f, s1 = 0.0f;
-  int r = slice;
-  for (; r + 16 < nparts; r += 32) {
+  int r = threadIdx.x;
+  for (; r + 256 < nparts; r += 512) {
     s0 += partial[((int64_t)r * 2 + which) * kD + col];
-    s1 += partial[((int64_t)(r + 16) * 2 + which) * kD + col];
+    s1 += partial[((int64_t)(r + 256) * 2 + which) * kD + col];
   }
   if (r < nparts) s0 += partial[((int64_t)r * 2 + which) * kD + col];
-  red[slice][col] = s0 + s1;
+  red[threadIdx.x] = s0 + s1;
   __syncthreads();
-  if (slice == 0) {
-    float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s += red[i][col];
-    (which == 0 ? dq_gain : dk_gain)[col] = s;
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
   }
+  if (threadIdx.x == 0) (which == 0 ? dq_gain : dk_gain)[col] = red[0];
 }
 
 int ntb_of(int T) { return (T + kBlockTokens - 1) / kBlockTokens; }
@@ -417,6 +417,6 @@ extern "C" int32_t algx_qk_prologue_bwd(const void* q, const void* k, const floa
                       dv_out, dq, dk, dv, partial, T, H, ntb, eps);
   if (int32_t rc = check_launch("qk_prologue_bwd")) return rc;
   if (!norm) return 0;
-  prologue_gain_finish<<<2, 1024, 0, s>>>(partial, B * ntb, dq_gain, dk_gain);
+  prologue_gain_finish<<<2 * kD, 256, 0, s>>>(partial, B * ntb, dq_gain, dk_gain);
   return check_launch("qk_prologue_gain_finish");
 }
