@@ -1,0 +1,229 @@
+"""Muon + AdamW, cautious AdamW and the hybrid, on PyTorch-ROCm tensors.
+
+Counterpart of ``algebraic.optimizers`` (src/algebraic/optimizers.py): the
+same ``newton_schulz_5``, ``is_muon_param``, ``make_cosine_schedule`` and
+``get_optimizer(name, lr, ...) -> (init_fn, step_fn)`` with the reference's
+update rules. The parameter trees are the model's dicts of float32 tensors;
+``step_fn`` updates parameters and state in place and returns them (the
+functional signature of the reference, without copying 1.4 GB per step).
+
+The Newton-Schulz products run as batched GEMMs over the layer-stacked
+weights (hipBLASLt through torch). ``ns_dtype`` selects their input type:
+bfloat16 (default; the reference's float32 matmuls run as single bfloat16
+passes on its TPUs at default precision) or float32.
+"""
+
+import math
+from typing import Any, Callable, Dict, Optional, Tuple
+
+import torch
+
+F32 = torch.float32
+
+
+_NS_ABC = (3.4445, -4.7750, 2.0315)
+
+
+def _ns_wide(X: torch.Tensor, steps: int, eps: float, ns_dtype: torch.dtype) -> torch.Tensor:
+    """Newton-Schulz on a batch (k, m, n), m <= n, without the aspect factor.
+
+    Each update is one batched GEMM with its linear combination folded into
+    the GEMM's own alpha/beta: B = b A + c A A and X <- a X + B X
+    (= baddbmm(X, B, X, beta=a)), X <- 1.5 X - 0.5 (X X^T) X for the
+    refinements; only X X^T needs X^T materialised."""
+    a, b, c = _NS_ABC
+    X = X.to(F32)
+    norm = torch.sqrt((X * X).sum(dim=(-2, -1), keepdim=True) + eps)
+    X = (X / norm).to(ns_dtype).contiguous()
+
+    def gram(x):
+        return torch.bmm(x, x.transpose(-2, -1).contiguous())
+
+    for _ in range(steps):
+        A = gram(X)
+        Bm = torch.baddbmm(A, A, A, beta=b, alpha=c)
+        X = torch.baddbmm(X, Bm, X, beta=a, alpha=1.0)
+    for _ in range(2):
+        X = torch.baddbmm(X, gram(X), X, beta=1.5, alpha=-0.5)
+    return X
+
+
+def newton_schulz_5(G: torch.Tensor, steps: int = 5, eps: float = 1e-7,
+                    ns_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Orthogonalise the trailing (M, N) matrices of G (optimizers.py:27-64):
+    Frobenius pre-normalisation, ``steps`` quintic iterations with
+    (a, b, c) = (3.4445, -4.7750, 2.0315), two order-3 Schulz refinements,
+    and the aspect-ratio factor sqrt(max(1, M/N)). Returns float32."""
+    if G.ndim < 2:
+        return G
+    M, N = G.shape[-2], G.shape[-1]
+    X = G.reshape((-1, M, N))
+    if M > N:
+        X = X.transpose(-2, -1)
+    X = _ns_wide(X, steps, eps, ns_dtype)
+    if M > N:
+        X = X.transpose(-2, -1)
+    return (X.to(F32) * math.sqrt(max(1.0, float(M) / float(N)))).reshape(G.shape)
+
+
+def newton_schulz_many(Gs, steps: int = 5, eps: float = 1e-7,
+                       ns_dtype: torch.dtype = torch.bfloat16):
+    """newton_schulz_5 of every tensor in Gs, the matrices of equal (oriented)
+    shape run as one batch: the model's 7 stacked weights become two batches
+    ([w_q | w_k | w_v | w_o] and [w_g | w_u | w_d^T])."""
+    groups: Dict[Tuple[int, int], list] = {}
+    for i, G in enumerate(Gs):
+        M, N = G.shape[-2], G.shape[-1]
+        X = G.reshape((-1, M, N))
+        if M > N:
+            X = X.transpose(-2, -1)
+        groups.setdefault(tuple(X.shape[-2:]), []).append((i, X))
+    out = [None] * len(Gs)
+    for items in groups.values():
+        batch = torch.cat([x for _, x in items], dim=0)
+        Y = _ns_wide(batch, steps, eps, ns_dtype)
+        k0 = 0
+        for i, x in items:
+            y = Y[k0:k0 + x.shape[0]]
+            k0 += x.shape[0]
+            G = Gs[i]
+            M, N = G.shape[-2], G.shape[-1]
+            if M > N:
+                y = y.transpose(-2, -1)
+            out[i] = (y.to(F32) * math.sqrt(max(1.0, float(M) / float(N)))).reshape(G.shape)
+    return out
+
+
+def is_muon_param(path, param) -> bool:
+    """Layer weight matrices take Muon; embedding, gains, sinks and biases the
+    Adam family (optimizers.py:67-89). ``path``: the key path (a tuple of
+    names) of the leaf."""
+    if path:
+        key = str(path[-1] if isinstance(path, (list, tuple)) else path)
+        if key == "embed":
+            return False
+        if key.startswith("w_"):
+            return True
+        if key.startswith("ln") or key.endswith("_gain") or key == "sink" or "bias" in key:
+            return False
+    return getattr(param, "ndim", 0) >= 2
+
+
+def make_cosine_schedule(peak_lr: float, total_steps: int, warmup_fraction: float,
+                         min_lr_ratio: float) -> Callable[[int], float]:
+    """Linear warmup then cosine decay to min_lr_ratio * peak (optimizers.py:92-115)."""
+    warm = (float(warmup_fraction) if warmup_fraction >= 1
+            else max(1.0, float(round(warmup_fraction * total_steps))))
+    floor = peak_lr * min_lr_ratio
+    total_t = float(total_steps)
+
+    def schedule(step) -> float:
+        t = float(step) + 1.0
+        if t < warm:
+            return peak_lr * min(1.0, t / warm)
+        prog = min(max((t - warm) / max(1.0, total_t - warm), 0.0), 1.0)
+        return floor + (peak_lr - floor) * 0.5 * (1.0 + math.cos(math.pi * prog))
+
+    return schedule
+
+
+def _flatten(tree, prefix=()):
+    if isinstance(tree, dict):
+        out = []
+        for k, v in tree.items():
+            out.extend(_flatten(v, prefix + (k,)))
+        return out
+    return [(prefix, tree)]
+
+
+def _get(tree, path):
+    for k in path:
+        tree = tree[k]
+    return tree
+
+
+class OptState:
+    """count, first moments m, second moments v (None for Muon leaves), keyed
+    by the leaf's key path (optimizers.py:20-24)."""
+
+    def __init__(self, count: int, m: Dict, v: Dict):
+        self.count, self.m, self.v = count, m, v
+
+
+def get_optimizer(name: str, lr: float, weight_decay: float = 0.1, total_steps: int = 1000,
+                  warmup_fraction: float = 0.02, min_lr_ratio: float = 0.1, b1: float = 0.9,
+                  b2: float = 0.95, adam_eps: float = 1e-8, muon_lr: Optional[float] = None,
+                  muon_wd: Optional[float] = None, muon_momentum: float = 0.95,
+                  muon_steps: int = 5, cautious_eps: float = 1e-3,
+                  ns_dtype: torch.dtype = torch.bfloat16, **kwargs: Any
+                  ) -> Tuple[Callable, Callable]:
+    """(init_fn, step_fn) for 'muon_adamw', 'cadamw' or 'hybrid_muon_cadamw'
+    (optimizers.py:118-246)."""
+    opt_name = name.lower().strip()
+    valid = ("muon_adamw", "cadamw", "hybrid_muon_cadamw")
+    if opt_name not in valid:
+        raise ValueError(f"Unknown optimizer: {name}. Choices: {valid}")
+    m_lr = lr if muon_lr is None else muon_lr
+    m_wd = weight_decay if muon_wd is None else muon_wd
+    adam_schedule = make_cosine_schedule(lr, total_steps, warmup_fraction, min_lr_ratio)
+    muon_schedule = make_cosine_schedule(m_lr, total_steps, warmup_fraction, min_lr_ratio)
+    uses_muon = opt_name in ("muon_adamw", "hybrid_muon_cadamw")
+
+    def init_fn(params) -> OptState:
+        m, v = {}, {}
+        for path, p in _flatten(params):
+            m[path] = torch.zeros_like(p, dtype=F32)
+            muon = uses_muon and is_muon_param(path, p)
+            v[path] = None if muon else torch.zeros_like(p, dtype=F32)
+        return OptState(0, m, v)
+
+    @torch.no_grad()
+    def step_fn(step: int, params, grads, opt_state: OptState, decay_mask):
+        adam_lr = adam_schedule(step)
+        muon_lr_t = muon_schedule(step)
+        t = float(step + 1)
+        c1, c2 = 1.0 - b1 ** t, 1.0 - b2 ** t
+        muon_jobs = []
+        for path, p in _flatten(params):
+            g = _get(grads, path)
+            if g is None:
+                continue
+            g = g.to(F32)
+            m, v = opt_state.m[path], opt_state.v[path]
+            decay = bool(_get(decay_mask, path))
+            if uses_muon and is_muon_param(path, p):
+                # m <- mu m + (1 - mu) g; Nesterov look-ahead; orthogonalised below
+                m.mul_(muon_momentum).add_(g, alpha=1.0 - muon_momentum)
+                muon_jobs.append((p, decay, g.mul(1.0 - muon_momentum).add_(m, alpha=muon_momentum)))
+                continue
+            m.mul_(b1).add_(g, alpha=1.0 - b1)
+            v.mul_(b2).addcmul_(g, g, value=1.0 - b2)
+            u = (m / c1) / (torch.sqrt(v / c2) + adam_eps)
+            if opt_name in ("cadamw", "hybrid_muon_cadamw"):
+                mask = (u * g > 0.0).to(F32)
+                u = u * (mask / torch.clamp(mask.mean(), min=cautious_eps))
+            if decay:
+                p.mul_(1.0 - adam_lr * weight_decay)
+            p.add_(u, alpha=-adam_lr)
+        if muon_jobs:
+            ortho = newton_schulz_many([look for _, _, look in muon_jobs], steps=muon_steps,
+                                       ns_dtype=ns_dtype)
+            for (p, decay, _), o in zip(muon_jobs, ortho):
+                if decay:
+                    p.mul_(1.0 - muon_lr_t * m_wd)
+                p.add_(o, alpha=-muon_lr_t)
+        opt_state.count += 1
+        return params, opt_state
+
+    return init_fn, step_fn
+
+
+def grads_of(params) -> Dict:
+    """The .grad tree of a parameter tree (None where a leaf has no gradient)."""
+    if isinstance(params, dict):
+        return {k: grads_of(v) for k, v in params.items()}
+    return params.grad
+
+
+__all__ = ["OptState", "newton_schulz_5", "newton_schulz_many", "is_muon_param",
+           "make_cosine_schedule", "get_optimizer", "grads_of"]

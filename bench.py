@@ -244,13 +244,16 @@ def model_flops_per_token(cfg, T):
     return 6 * dense + 3.5 * L * 2 * H * T * D
 
 
-def bench_model(preset, steps, warmup, dev, B=8, T=2048, V=50304, remat=True):
+def bench_model(preset, steps, warmup, dev, B=8, T=2048, V=50304, remat=True, optimizer=False):
     """one forward + backward of the 350M preset (d 1024, 24 layers,
     16 heads of 64, d_ff 2688, V 50304) on B x T random tokens, random-init
     weights, bf16; parameter gradients are produced (no optimiser update).
     remat=True recomputes each block in the backward as the reference's
     default LMConfig does; remat=False keeps the activations (they fit in HBM
-    at this size many times over)."""
+    at this size many times over). optimizer=True adds the reference trainer's
+    default update, Muon on the layer matrices + AdamW on the rest
+    (optimizers.py:118-246, lr 2e-3 as configs/comparison_350m.json), to
+    every step: a full training step."""
     import torch
     from algebraic_amd import config, model
     # Plain library GEMMs: torch's TunableOp picks, per projection shape, the
@@ -275,16 +278,27 @@ def bench_model(preset, steps, warmup, dev, B=8, T=2048, V=50304, remat=True):
     x, y = tok[:, :-1].contiguous(), tok[:, 1:].contiguous()
     tables = model.position_tables(cfg, T, device=dev)
 
+    opt = None
+    if optimizer:
+        from algebraic_amd import optimizers
+        init_fn, step_fn = optimizers.get_optimizer("muon_adamw", 2e-3, weight_decay=0.1)
+        opt = [init_fn(params), 0]
+        mask = model.decay_mask(params)
+
     def step():
         for t in leaves:
             t.grad = None
         obj, _ = model.train_objective(params, x, y, cfg, tables)
         obj.backward()
+        if opt is not None:
+            step_fn(opt[1], params, optimizers.grads_of(params), opt[0], mask)
+            opt[1] += 1
 
     fpt = model_flops_per_token(cfg, T)
     torch.cuda.reset_peak_memory_stats()
     dt = time_steps(step, steps, warmup)
-    out = {"workload": f"configs[4] {preset} 350M fwd+bwd, B={B}, T={T}, V={V}, bf16, "
+    what = "train step (fwd+bwd+Muon/AdamW)" if optimizer else "fwd+bwd"
+    out = {"workload": f"configs[4] {preset} 350M {what}, B={B}, T={T}, V={V}, bf16, "
                        f"{'remat' if remat else 'no remat'}",
            "peak_hbm_gb": torch.cuda.max_memory_allocated() / 1e9,
            "ms_per_step": dt * 1e3, "tokens_per_s": B * T / dt,
@@ -358,11 +372,13 @@ def main():
               flush=True)
         return
     if args.model_only:
-        for preset, remat in (("algebraic", False), ("standard", False), ("algebraic", True),
-                              ("standard", True)):
+        for preset, remat, opt in (("algebraic", False, False), ("standard", False, False),
+                                   ("algebraic", True, False), ("standard", True, False),
+                                   ("algebraic", False, True)):
             print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
                               for k, v in bench_model(preset, args.steps, args.warmup, dev,
-                                                      remat=remat).items()}), flush=True)
+                                                      remat=remat, optimizer=opt).items()}),
+                  flush=True)
         return
     if args.elementwise_only:
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
@@ -428,10 +444,12 @@ def main():
             "elementwise": {k: (round(v, 4) if isinstance(v, float) else v)
                             for k, v in bench_elementwise(20, 3, dev).items()},
         }
-        for preset, remat in (("algebraic", False), ("standard", False), ("algebraic", True)):
-            line["secondary"][f"model_350m_{preset}{'_remat' if remat else ''}"] = {
+        for preset, remat, opt in (("algebraic", False, False), ("standard", False, False),
+                                   ("algebraic", True, False), ("algebraic", False, True)):
+            key = f"model_350m_{preset}{'_remat' if remat else ''}{'_train' if opt else ''}"
+            line["secondary"][key] = {
                 k: (round(v, 4) if isinstance(v, float) else v)
-                for k, v in bench_model(preset, 5, 2, dev, remat=remat).items()}
+                for k, v in bench_model(preset, 5, 2, dev, remat=remat, optimizer=opt).items()}
     if not args.no_cpu:
         line["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                 for k, v in cpu_baseline(B, H, T, D).items()}
