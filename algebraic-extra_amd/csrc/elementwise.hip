@@ -170,20 +170,32 @@ __global__ __launch_bounds__(kBwdThreads) void rmsnorm_bwd_kernel(
   }
 }
 
-// dgain[col] = sum of the workgroup partials: 64 columns per workgroup, four
-// interleaved slices of the partial rows per column, combined in slice order.
-__global__ __launch_bounds__(256) void rmsnorm_gain_finish(const float* __restrict__ partial,
-                                                           int nparts, int D,
-                                                           float* __restrict__ dgain) {
-  __shared__ float red[4][64];
+// dgain[col] = sum of the workgroup partials: 64 columns per workgroup of
+// 1024 threads, 16 interleaved slices of the partial rows per column (many
+// independent loads in flight), combined in slice order (deterministic).
+__global__ __launch_bounds__(1024) void rmsnorm_gain_finish(const float* __restrict__ partial,
+                                                            int nparts, int D,
+                                                            float* __restrict__ dgain) {
+  __shared__ float red[16][64];
   const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
   const int col = blockIdx.x * 64 + lane;
-  float s = 0.0f;
-  if (col < D)
-    for (int b = slice; b < nparts; b += 4) s += partial[(int64_t)b * D + col];
-  red[slice][lane] = s;
+  float s0 = 0.0f, s1 = 0.0f;
+  if (col < D) {
+    int r = slice;
+    for (; r + 16 < nparts; r += 32) {
+      s0 += partial[(int64_t)r * D + col];
+      s1 += partial[(int64_t)(r + 16) * D + col];
+    }
+    if (r < nparts) s0 += partial[(int64_t)r * D + col];
+  }
+  red[slice][lane] = s0 + s1;
   __syncthreads();
-  if (slice == 0 && col < D) dgain[col] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+  if (slice == 0 && col < D) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += red[i][lane];
+    dgain[col] = s;
+  }
 }
 
 // alu in float32 (algebraic.py:86-93): u = bz r, r = rsqrt(1 + (bz)^2),
@@ -410,7 +422,7 @@ extern "C" int32_t algx_rms_norm_bwd(const void* x, const float* gain, const voi
   }
   if (int32_t rc = check_launch("rms_norm_bwd")) return rc;
   if (gain == nullptr) return 0;
-  rmsnorm_gain_finish<<<(D + 63) / 64, 256, 0, s>>>(partial, bwd_blocks(rows), D, dgain);
+  rmsnorm_gain_finish<<<(D + 63) / 64, 1024, 0, s>>>(partial, bwd_blocks(rows), D, dgain);
   return check_launch("rms_norm_gain_finish");
 }
 
