@@ -59,6 +59,8 @@ SIGNATURES = {
     "algx_rms_norm_fwd": (_i32, [_p, _p, _p, _i64, _i32, _i32, _f32, _p]),
     "algx_rms_norm_bwd_workspace_bytes": (_i64, [_i64, _i32, _i32]),
     "algx_rms_norm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _f32, _p]),
+    "algx_add_rms_norm_fwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _i32, _f32, _p]),
+    "algx_add_rms_norm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _f32, _p]),
     "algx_alu_fwd": (_i32, [_p, _p, _i64, _i32, _f32, _p]),
     "algx_alu_bwd": (_i32, [_p, _p, _p, _i64, _i32, _f32, _p]),
     "algx_alu_glu_fwd": (_i32, [_p, _p, _p, _i64, _i32, _f32, _p]),

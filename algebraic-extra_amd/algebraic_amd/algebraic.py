@@ -76,6 +76,61 @@ def rms_norm(x: torch.Tensor, gain: Optional[torch.Tensor], eps: float = 1e-5) -
     return _RMSNormFn.apply(_aligned(x), g32, float(eps))
 
 
+class _AddRMSNormFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, r, gain, eps):
+        D = x.shape[-1]
+        rows = x.numel() // D if D else 0
+        xsum, y = torch.empty_like(x), torch.empty_like(x)
+        _lib.call("algx_add_rms_norm_fwd", _lib.ptr(x), _lib.ptr(r), _lib.ptr(gain),
+                  _lib.ptr(xsum), _lib.ptr(y), rows, D, _lib.dtype_code(x.dtype), float(eps),
+                  _lib.stream())
+        ctx.eps = eps
+        ctx.save_for_backward(xsum, gain)
+        return xsum, y
+
+    @staticmethod
+    def backward(ctx, dxsum, dy):
+        xsum, gain = ctx.saved_tensors
+        D = xsum.shape[-1]
+        rows = xsum.numel() // D if D else 0
+        dt = _lib.dtype_code(xsum.dtype)
+        dy = torch.zeros_like(xsum) if dy is None else _aligned(dy.to(xsum.dtype))
+        dres = torch.zeros_like(xsum) if dxsum is None else _aligned(dxsum.to(xsum.dtype))
+        dx = torch.empty_like(xsum)
+        dgain = ws = None
+        if gain is not None:
+            dgain = torch.empty(D, dtype=torch.float32, device=xsum.device)
+            ws = torch.empty(max(1, _lib.query("algx_rms_norm_bwd_workspace_bytes", rows, D, dt)),
+                             dtype=torch.uint8, device=xsum.device)
+        _lib.call("algx_add_rms_norm_bwd", _lib.ptr(xsum), _lib.ptr(gain), _lib.ptr(dy),
+                  _lib.ptr(dres), _lib.ptr(dx), _lib.ptr(dgain), _lib.ptr(ws), rows, D, dt,
+                  float(ctx.eps), _lib.stream())
+        return dx, dx, dgain, None
+
+
+def add_rms_norm(x: torch.Tensor, r: torch.Tensor, gain: Optional[torch.Tensor],
+                 eps: float = 1e-5):
+    """``(s, rms_norm(s, gain))`` for the residual sum ``s = x + r`` in one
+    pass (the block's residual add followed by the next norm, model.py:177-178,
+    :191, :166), rounded as the unfused add and norm round."""
+    if x.shape != r.shape or x.dtype != r.dtype:
+        raise ValueError("add_rms_norm needs x and r of one shape and dtype")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("rms_norm kernel needs float32 or bfloat16 input")
+    D = x.shape[-1] if x.ndim else 0
+    width = 8 if x.dtype == torch.bfloat16 else 4
+    if D <= 0 or D % width or D > 1024:
+        raise NotImplementedError(f"rms_norm kernel needs a last axis that is a multiple of {width}"
+                                  f" and at most 1024, got {D}")
+    if gain is not None and tuple(gain.shape) != (D,):
+        raise ValueError(f"gain must have shape ({D},)")
+    if not eps > 0:
+        raise ValueError("rms_norm epsilon must be positive")
+    g32 = None if gain is None else gain.to(torch.float32).contiguous()
+    return _AddRMSNormFn.apply(_aligned(x), _aligned(r), g32, float(eps))
+
+
 class _ALUFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, beta):

@@ -25,7 +25,7 @@ import torch
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
-from .algebraic import glu_packed, rms_norm
+from .algebraic import add_rms_norm, glu_packed, rms_norm
 from .kernels.flash import flash_attention
 from .kernels.fused_head import fused_head
 from .kernels.prologue import attention_prologue
@@ -284,12 +284,26 @@ def _qkv(cfg: LMConfig, cos, sin, h, lp):
     return apply_rotary(q, cos, sin), apply_rotary(k, cos, sin), v
 
 
-def _block(cfg: LMConfig, cos, sin, x, lp):
-    """One pre-norm block (model.py:162-191)."""
+def _add_norm(x, r, gain, cfg: LMConfig):
+    """(x + r, norm(x + r)) in one pass; r None: (x, norm(x))."""
+    g = gain if cfg.norm == "rms" else None
+    if r is None:
+        return x, rms_norm(x, g, cfg.eps)
+    return add_rms_norm(x, r, g, cfg.eps)
+
+
+def _block(cfg: LMConfig, cos, sin, x, r, lp):
+    """One pre-norm block (model.py:162-191) on the residual stream x + r.
+
+    The block's two residual adds are fused into the norms that read their
+    sums: x + r (the previous block's feed-forward output, added here) with
+    ln1, and x + attention with ln2. It returns (x, y): the stream after
+    attention and this block's feed-forward output, still to be added by the
+    next norm. Sums and roundings are those of model.py:177 and :191."""
     B, T, d = x.shape
     H = cfg.n_heads
     dt = x.dtype
-    h = _norm(x, lp.get("ln1"), cfg)
+    x, h = _add_norm(x, r, lp.get("ln1"), cfg)
     q, k, v = _qkv(cfg, cos, sin, h, lp)
     if cfg.sink == "learned":
         sink = lp["sink"].to(F32)
@@ -299,15 +313,14 @@ def _block(cfg: LMConfig, cos, sin, x, lp):
         sink = None
     a = _attention(q, k, v, sink, cfg)
     a = a.transpose(1, 2).reshape(B, T, d)
-    x = x + a @ lp["w_o"].to(dt)
-    h2 = _norm(x, lp.get("ln2"), cfg)
+    x, h2 = _add_norm(x, a @ lp["w_o"].to(dt), lp.get("ln2"), cfg)
     if cfg.ffn not in ("swiglu", "alu_glu"):
         raise ValueError(f"unknown ffn {cfg.ffn!r}")
     # gate and up from one GEMM against [w_g | w_u]; the gated product reads
     # its rows in place and returns the gradient packed the same way.
     gu = h2 @ torch.cat([lp["w_g"], lp["w_u"]], dim=1).to(dt)
     y = glu_packed(gu, "alu" if cfg.ffn == "alu_glu" else "silu", cfg.alu_beta)
-    return x + y @ lp["w_d"].to(dt)
+    return x, y @ lp["w_d"].to(dt)
 
 
 def forward_hidden(params, tokens: torch.Tensor, cfg: LMConfig, tables) -> torch.Tensor:
@@ -319,13 +332,14 @@ def forward_hidden(params, tokens: torch.Tensor, cfg: LMConfig, tables) -> torch
     # in one pass, where indexing t[i] per layer would materialise (and add)
     # a zero-filled full-size gradient for every layer.
     per_layer = {name: t.unbind(0) for name, t in params["layers"].items()}
+    r = None
     for i in range(cfg.n_layers):
         lp = {name: ts[i] for name, ts in per_layer.items()}
         if cfg.remat:
-            x = checkpoint(_block, cfg, cos, sin, x, lp, use_reentrant=False)
+            x, r = checkpoint(_block, cfg, cos, sin, x, r, lp, use_reentrant=False)
         else:
-            x = _block(cfg, cos, sin, x, lp)
-    return _norm(x, params.get("final_gain"), cfg)
+            x, r = _block(cfg, cos, sin, x, r, lp)
+    return _add_norm(x, r, params.get("final_gain"), cfg)[1]
 
 
 # ---------------------------------------------------------------------------

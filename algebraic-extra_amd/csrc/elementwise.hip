@@ -49,12 +49,16 @@ __device__ __forceinline__ void load_gain(const float* gain, int lane, int nch,
 }
 
 // y = cast((x * tau) * gain), tau = rsqrt(mean(x^2) + eps) (algebraic.py:76-83).
-// One row per wave; CPL = 16-byte chunks per lane.
+// One row per wave; CPL = 16-byte chunks per lane. With a residual r the row
+// is first x = cast(x + r) (the block's residual add, model.py:177, :191),
+// written to xsum, and normalised.
 template <typename T, int CPL>
 __global__ __launch_bounds__(kFwdThreads) void rmsnorm_fwd_kernel(const T* __restrict__ x,
                                                                   const float* __restrict__ gain,
                                                                   T* __restrict__ y, int64_t rows,
-                                                                  int D, float eps) {
+                                                                  int D, float eps,
+                                                                  const T* __restrict__ r,
+                                                                  T* __restrict__ xsum) {
   typedef typename Vec<T>::type VT;
   constexpr int EPL = Vec<T>::n;
   const int lane = threadIdx.x & 63;
@@ -73,6 +77,12 @@ __global__ __launch_bounds__(kFwdThreads) void rmsnorm_fwd_kernel(const T* __res
       const int ch = lane + 64 * c;
       if (ch < nch) {
         in[c] = *reinterpret_cast<const VT*>(xr + ch * EPL);
+        if (r != nullptr) {
+          const VT rv = *reinterpret_cast<const VT*>(r + row * D + ch * EPL);
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) in[c][e] = from_f<T>(to_f(in[c][e]) + to_f(rv[e]));
+          *reinterpret_cast<VT*>(xsum + row * D + ch * EPL) = in[c];
+        }
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
           const float f = to_f(in[c][e]);
@@ -99,10 +109,14 @@ __global__ __launch_bounds__(kFwdThreads) void rmsnorm_fwd_kernel(const T* __res
 //   dx = tau * gain * dy - x * tau^3 * sum(dy * gain * x) / D
 // and, given `partial` ([gridDim.x][D] float32), each workgroup's share of
 //   dgain = sum_rows dy * x * tau.
+// With dres (the gradient reaching the normalised input along the residual
+// stream) the output is cast(cast(dx) + dres): autograd's sum of the two
+// gradients of the residual sum, rounded as it rounds.
 template <typename T, int CPL>
 __global__ __launch_bounds__(kBwdThreads) void rmsnorm_bwd_kernel(
     const T* __restrict__ x, const float* __restrict__ gain, const T* __restrict__ dy,
-    T* __restrict__ dx, float* __restrict__ partial, int64_t rows, int D, float eps) {
+    T* __restrict__ dx, float* __restrict__ partial, int64_t rows, int D, float eps,
+    const T* __restrict__ dres) {
   typedef typename Vec<T>::type VT;
   constexpr int EPL = Vec<T>::n;
   __shared__ float red[kBwdWaves][kMaxD];
@@ -147,6 +161,11 @@ __global__ __launch_bounds__(kBwdThreads) void rmsnorm_bwd_kernel(
           const float xf = to_f(xi[c][e]), df = to_f(gi[c][e]);
           out[e] = from_f<T>(tau * g[c][e] * df - cfac * xf);
           dg[c][e] = __builtin_fmaf(df, xf * tau, dg[c][e]);
+        }
+        if (dres != nullptr) {
+          const VT rv = *reinterpret_cast<const VT*>(dres + row * D + ch * EPL);
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) out[e] = from_f<T>(to_f(out[e]) + to_f(rv[e]));
         }
         *reinterpret_cast<VT*>(dx + row * D + ch * EPL) = out;
       }
@@ -354,16 +373,17 @@ int32_t check_aligned(std::initializer_list<const void*> ps, const char* what) {
 
 template <typename T, int CPL>
 void launch_norm_fwd(const void* x, const float* gain, void* y, int64_t rows, int D, float eps,
-                     hipStream_t s) {
+                     const void* r, void* xsum, hipStream_t s) {
   launch_k(probe_for(ALGX_PROBE_RMSNORM_FWD), rmsnorm_fwd_kernel<T, CPL>, dim3(fwd_blocks(rows)),
-           dim3(kFwdThreads), s, (const T*)x, gain, (T*)y, rows, D, eps);
+           dim3(kFwdThreads), s, (const T*)x, gain, (T*)y, rows, D, eps, (const T*)r, (T*)xsum);
 }
 
 template <typename T, int CPL>
 void launch_norm_bwd(const void* x, const float* gain, const void* dy, void* dx, float* partial,
-                     int64_t rows, int D, float eps, hipStream_t s) {
+                     int64_t rows, int D, float eps, const void* dres, hipStream_t s) {
   launch_k(probe_for(ALGX_PROBE_RMSNORM_BWD), rmsnorm_bwd_kernel<T, CPL>, dim3(bwd_blocks(rows)),
-           dim3(kBwdThreads), s, (const T*)x, gain, (const T*)dy, (T*)dx, partial, rows, D, eps);
+           dim3(kBwdThreads), s, (const T*)x, gain, (const T*)dy, (T*)dx, partial, rows, D, eps,
+           (const T*)dres);
 }
 
 }  // namespace
@@ -371,25 +391,72 @@ void launch_norm_bwd(const void* x, const float* gain, const void* dy, void* dx,
 
 using namespace algx;
 
-extern "C" int32_t algx_rms_norm_fwd(const void* x, const float* gain, void* y, int64_t rows,
-                                     int32_t D, int32_t dtype, float eps, void* stream) {
+namespace {
+
+int32_t norm_fwd_impl(const void* x, const void* r, const float* gain, void* xsum, void* y,
+                      int64_t rows, int32_t D, int32_t dtype, float eps, hipStream_t s) {
   if (int32_t rc = check_norm(x, rows, D, dtype, eps)) return rc;
   if (rows == 0) return 0;
   if (y == nullptr) return fail("rms_norm: null output");
+  if (r != nullptr && xsum == nullptr) return fail("rms_norm: the residual sum needs xsum");
   if (int32_t rc = check_aligned({x, y}, "rms_norm")) return rc;
-  hipStream_t s = (hipStream_t)stream;
+  if (r != nullptr)
+    if (int32_t rc = check_aligned({r, xsum}, "rms_norm")) return rc;
   // Chunks per lane: ceil(D / (16-byte elements) / 64).
   const int cpl = (D / epl_of(dtype) + 63) / 64;
   if (dtype == ALGX_BF16) {
-    if (cpl == 1) launch_norm_fwd<bf16, 1>(x, gain, y, rows, D, eps, s);
-    else launch_norm_fwd<bf16, 2>(x, gain, y, rows, D, eps, s);
+    if (cpl == 1) launch_norm_fwd<bf16, 1>(x, gain, y, rows, D, eps, r, xsum, s);
+    else launch_norm_fwd<bf16, 2>(x, gain, y, rows, D, eps, r, xsum, s);
   } else {
-    if (cpl == 1) launch_norm_fwd<float, 1>(x, gain, y, rows, D, eps, s);
-    else if (cpl == 2) launch_norm_fwd<float, 2>(x, gain, y, rows, D, eps, s);
-    else if (cpl == 3) launch_norm_fwd<float, 3>(x, gain, y, rows, D, eps, s);
-    else launch_norm_fwd<float, 4>(x, gain, y, rows, D, eps, s);
+    if (cpl == 1) launch_norm_fwd<float, 1>(x, gain, y, rows, D, eps, r, xsum, s);
+    else if (cpl == 2) launch_norm_fwd<float, 2>(x, gain, y, rows, D, eps, r, xsum, s);
+    else if (cpl == 3) launch_norm_fwd<float, 3>(x, gain, y, rows, D, eps, r, xsum, s);
+    else launch_norm_fwd<float, 4>(x, gain, y, rows, D, eps, r, xsum, s);
   }
   return check_launch("rms_norm_fwd");
+}
+
+int32_t norm_bwd_impl(const void* x, const float* gain, const void* dy, const void* dres,
+                      void* dx, float* dgain, void* workspace, int64_t rows, int32_t D,
+                      int32_t dtype, float eps, hipStream_t s) {
+  if (int32_t rc = check_norm(x, rows, D, dtype, eps)) return rc;
+  if ((gain == nullptr) != (dgain == nullptr))
+    return fail("rms_norm: dgain is required exactly when gain is given");
+  if (rows == 0) return dgain != nullptr ? fill_f32(dgain, D, 0.0f, s) : 0;
+  if (dy == nullptr || dx == nullptr) return fail("rms_norm: null dy/dx");
+  if (gain != nullptr && workspace == nullptr) return fail("rms_norm: null workspace");
+  if (int32_t rc = check_aligned({x, dy, dx}, "rms_norm")) return rc;
+  if (dres != nullptr)
+    if (int32_t rc = check_aligned({dres}, "rms_norm")) return rc;
+  float* partial = gain != nullptr ? (float*)workspace : nullptr;
+  const int cpl = (D / epl_of(dtype) + 63) / 64;
+  if (dtype == ALGX_BF16) {
+    if (cpl == 1) launch_norm_bwd<bf16, 1>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
+    else launch_norm_bwd<bf16, 2>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
+  } else {
+    if (cpl == 1) launch_norm_bwd<float, 1>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
+    else if (cpl == 2) launch_norm_bwd<float, 2>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
+    else if (cpl == 3) launch_norm_bwd<float, 3>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
+    else launch_norm_bwd<float, 4>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
+  }
+  if (int32_t rc = check_launch("rms_norm_bwd")) return rc;
+  if (gain == nullptr) return 0;
+  rmsnorm_gain_finish<<<(D + 63) / 64, 1024, 0, s>>>(partial, bwd_blocks(rows), D, dgain);
+  return check_launch("rms_norm_gain_finish");
+}
+
+}  // namespace
+
+extern "C" int32_t algx_rms_norm_fwd(const void* x, const float* gain, void* y, int64_t rows,
+                                     int32_t D, int32_t dtype, float eps, void* stream) {
+  return norm_fwd_impl(x, nullptr, gain, nullptr, y, rows, D, dtype, eps, (hipStream_t)stream);
+}
+
+extern "C" int32_t algx_add_rms_norm_fwd(const void* x, const void* r, const float* gain,
+                                         void* xsum, void* y, int64_t rows, int32_t D,
+                                         int32_t dtype, float eps, void* stream) {
+  if (rows > 0 && r == nullptr) return fail("add_rms_norm: null residual");
+  return norm_fwd_impl(x, r, gain, xsum, y, rows, D, dtype, eps, (hipStream_t)stream);
 }
 
 extern "C" int64_t algx_rms_norm_bwd_workspace_bytes(int64_t rows, int32_t D, int32_t dtype) {
@@ -401,29 +468,17 @@ extern "C" int64_t algx_rms_norm_bwd_workspace_bytes(int64_t rows, int32_t D, in
 extern "C" int32_t algx_rms_norm_bwd(const void* x, const float* gain, const void* dy, void* dx,
                                      float* dgain, void* workspace, int64_t rows, int32_t D,
                                      int32_t dtype, float eps, void* stream) {
-  if (int32_t rc = check_norm(x, rows, D, dtype, eps)) return rc;
-  if ((gain == nullptr) != (dgain == nullptr))
-    return fail("rms_norm: dgain is required exactly when gain is given");
-  hipStream_t s = (hipStream_t)stream;
-  if (rows == 0) return dgain != nullptr ? fill_f32(dgain, D, 0.0f, s) : 0;
-  if (dy == nullptr || dx == nullptr) return fail("rms_norm: null dy/dx");
-  if (gain != nullptr && workspace == nullptr) return fail("rms_norm: null workspace");
-  if (int32_t rc = check_aligned({x, dy, dx}, "rms_norm")) return rc;
-  float* partial = gain != nullptr ? (float*)workspace : nullptr;
-  const int cpl = (D / epl_of(dtype) + 63) / 64;
-  if (dtype == ALGX_BF16) {
-    if (cpl == 1) launch_norm_bwd<bf16, 1>(x, gain, dy, dx, partial, rows, D, eps, s);
-    else launch_norm_bwd<bf16, 2>(x, gain, dy, dx, partial, rows, D, eps, s);
-  } else {
-    if (cpl == 1) launch_norm_bwd<float, 1>(x, gain, dy, dx, partial, rows, D, eps, s);
-    else if (cpl == 2) launch_norm_bwd<float, 2>(x, gain, dy, dx, partial, rows, D, eps, s);
-    else if (cpl == 3) launch_norm_bwd<float, 3>(x, gain, dy, dx, partial, rows, D, eps, s);
-    else launch_norm_bwd<float, 4>(x, gain, dy, dx, partial, rows, D, eps, s);
-  }
-  if (int32_t rc = check_launch("rms_norm_bwd")) return rc;
-  if (gain == nullptr) return 0;
-  rmsnorm_gain_finish<<<(D + 63) / 64, 1024, 0, s>>>(partial, bwd_blocks(rows), D, dgain);
-  return check_launch("rms_norm_gain_finish");
+  return norm_bwd_impl(x, gain, dy, nullptr, dx, dgain, workspace, rows, D, dtype, eps,
+                       (hipStream_t)stream);
+}
+
+extern "C" int32_t algx_add_rms_norm_bwd(const void* xsum, const float* gain, const void* dy,
+                                         const void* dres, void* dx, float* dgain,
+                                         void* workspace, int64_t rows, int32_t D, int32_t dtype,
+                                         float eps, void* stream) {
+  if (rows > 0 && dres == nullptr) return fail("add_rms_norm: null residual gradient");
+  return norm_bwd_impl(xsum, gain, dy, dres, dx, dgain, workspace, rows, D, dtype, eps,
+                       (hipStream_t)stream);
 }
 
 namespace {

@@ -171,6 +171,16 @@ int32_t algx_head_bwd(const void* h, const void* E, const int32_t* targets, cons
 int32_t algx_rms_norm_fwd(const void* x, const float* gain, void* y, int64_t rows, int32_t D,
                           int32_t dtype, float eps, void* stream);
 int64_t algx_rms_norm_bwd_workspace_bytes(int64_t rows, int32_t D, int32_t dtype);
+/* The block's residual add fused in front of the norm (model.py:177-178,
+ * :191 then the next block's :166): xsum = cast(x + r), y = rms_norm(xsum).
+ * Backward: dx = cast(cast(rms_norm VJP of dy) + dres), where dres is the
+ * gradient reaching xsum along the residual stream; dx is the gradient of
+ * both x and r. Same sizes, workspace and dgain rules as rms_norm. */
+int32_t algx_add_rms_norm_fwd(const void* x, const void* r, const float* gain, void* xsum, void* y,
+                              int64_t rows, int32_t D, int32_t dtype, float eps, void* stream);
+int32_t algx_add_rms_norm_bwd(const void* xsum, const float* gain, const void* dy, const void* dres,
+                              void* dx, float* dgain, void* workspace, int64_t rows, int32_t D,
+                              int32_t dtype, float eps, void* stream);
 int32_t algx_rms_norm_bwd(const void* x, const float* gain, const void* dy, void* dx,
                           float* dgain, void* workspace, int64_t rows, int32_t D, int32_t dtype,
                           float eps, void* stream);

@@ -209,3 +209,35 @@ def test_glu_packed_silu_matches_oracle(dtype, rows, f):
     want_dg, want_du = OE.swiglu_vjp(g, u, d, dtype)
     _check(dtype)(t.grad[:, :f], want_dg, what="dgate")
     _check(dtype)(t.grad[:, f:], want_du, what="dup")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("with_gain", [True, False])
+def test_add_rms_norm_equals_add_then_norm(dtype, with_gain):
+    """The fused residual add + norm gives the unfused x + r and rms_norm's
+    output bit for bit, and the same gradients (x's and r's are both the
+    sum's): dx bit for bit, dgain to float32 reduction order."""
+    from algebraic_amd.algebraic import add_rms_norm
+    rng = np.random.default_rng(31)
+    shape = (2, 300, 1024)
+    x, r = _randn(rng, shape, dtype, 2.0).to(DEV), _randn(rng, shape, dtype).to(DEV)
+    dsum, dy = _randn(rng, shape, dtype).to(DEV), _randn(rng, shape, dtype).to(DEV)
+    gain = (torch.from_numpy((1 + 0.1 * rng.standard_normal(1024)).astype(np.float32)).to(DEV)
+            if with_gain else None)
+    outs, grads = [], []
+    for fused in (True, False):
+        tx, tr = x.clone().requires_grad_(True), r.clone().requires_grad_(True)
+        tg = gain.clone().requires_grad_(True) if with_gain else None
+        if fused:
+            s, y = add_rms_norm(tx, tr, tg)
+        else:
+            s = tx + tr
+            y = rms_norm(s, tg)
+        torch.autograd.backward((s, y), (dsum, dy))
+        outs.append((s.detach(), y.detach()))
+        grads.append((tx.grad, tr.grad, tg.grad if with_gain else None))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+    if with_gain:
+        assert rel_l2(grads[0][2], grads[1][2]) <= 1e-6
