@@ -270,8 +270,7 @@ def _qkv(cfg: LMConfig, cos, sin, h, lp):
     H, D = cfg.n_heads, cfg.head_dim
     dt = h.dtype
     if D == 64:
-        w = torch.cat([lp["w_q"], lp["w_k"], lp["w_v"]], dim=1).to(dt)
-        qkv = h @ w
+        qkv = h @ lp["w_qkv"]
         gains = (lp["q_gain"], lp["k_gain"]) if cfg.qk_norm else (None, None)
         tabs = (None, None) if cfg.pos == "none" else (cos, sin)
         return attention_prologue(qkv, H, gains[0], gains[1], tabs[0], tabs[1], cfg.eps)
@@ -313,14 +312,14 @@ def _block(cfg: LMConfig, cos, sin, x, r, lp):
         sink = None
     a = _attention(q, k, v, sink, cfg)
     a = a.transpose(1, 2).reshape(B, T, d)
-    x, h2 = _add_norm(x, a @ lp["w_o"].to(dt), lp.get("ln2"), cfg)
+    x, h2 = _add_norm(x, a @ lp["w_o_c"], lp.get("ln2"), cfg)
     if cfg.ffn not in ("swiglu", "alu_glu"):
         raise ValueError(f"unknown ffn {cfg.ffn!r}")
     # gate and up from one GEMM against [w_g | w_u]; the gated product reads
     # its rows in place and returns the gradient packed the same way.
-    gu = h2 @ torch.cat([lp["w_g"], lp["w_u"]], dim=1).to(dt)
+    gu = h2 @ lp["w_gu"]
     y = glu_packed(gu, "alu" if cfg.ffn == "alu_glu" else "silu", cfg.alu_beta)
-    return x, y @ lp["w_d"].to(dt)
+    return x, y @ lp["w_d_c"]
 
 
 def forward_hidden(params, tokens: torch.Tensor, cfg: LMConfig, tables) -> torch.Tensor:
@@ -330,8 +329,19 @@ def forward_hidden(params, tokens: torch.Tensor, cfg: LMConfig, tables) -> torch
     x = _norm(x, params.get("embed_gain"), cfg)
     # One unbind per stacked leaf: its backward stacks the per-layer gradients
     # in one pass, where indexing t[i] per layer would materialise (and add)
-    # a zero-filled full-size gradient for every layer.
-    per_layer = {name: t.unbind(0) for name, t in params["layers"].items()}
+    # a zero-filled full-size gradient for every layer. The matrices are cast
+    # to the compute dtype once per step for all layers (the reference casts
+    # per block, model.py:167-191: the same values), q/k/v and gate/up
+    # concatenated for their fused GEMMs.
+    layers = params["layers"]
+    dt = cfg.compute_dtype
+    per_layer = {name: t.unbind(0) for name, t in layers.items()}
+    per_layer["w_o_c"] = layers["w_o"].to(dt).unbind(0)
+    per_layer["w_d_c"] = layers["w_d"].to(dt).unbind(0)
+    per_layer["w_gu"] = torch.cat([layers["w_g"], layers["w_u"]], dim=2).to(dt).unbind(0)
+    if cfg.head_dim == 64:
+        per_layer["w_qkv"] = torch.cat([layers["w_q"], layers["w_k"], layers["w_v"]],
+                                       dim=2).to(dt).unbind(0)
     r = None
     for i in range(cfg.n_layers):
         lp = {name: ts[i] for name, ts in per_layer.items()}
