@@ -1,7 +1,7 @@
 // Fused tied-embedding projection + likelihood loss (fused_head.py) on gfx950.
 //
 // Forward (fused_head.py:72-117, :174-191): logits z^T = E h^T are formed
-// tile by tile (128 vocab x 128 tokens, d streamed through LDS in 64-wide
+// tile by tile (256 vocab x 256 tokens, d streamed through LDS in 32-wide
 // stages, v_mfma_f32_32x32x16_bf16) and never stored. Vocabulary rows sit on
 // the MFMA M axis so every lane holds 16 vocabulary values of one token; the
 // per-token statistic (online max/sum-exp for "ce", sum of rho(min(z/c,X))^n
