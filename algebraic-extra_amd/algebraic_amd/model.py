@@ -30,6 +30,7 @@ from .kernels.flash import flash_attention
 from .kernels.fused_head import fused_head
 from .kernels.prologue import attention_prologue
 from .kernels.qk_norm import qk_rms_norm
+from .layout import heads_to_tokens
 
 F32 = torch.float32
 _DTYPES = {"bfloat16": torch.bfloat16, "float32": torch.float32}
@@ -299,9 +300,7 @@ def _block(cfg: LMConfig, cos, sin, x, r, lp):
     ln1, and x + attention with ln2. It returns (x, y): the stream after
     attention and this block's feed-forward output, still to be added by the
     next norm. Sums and roundings are those of model.py:177 and :191."""
-    B, T, d = x.shape
     H = cfg.n_heads
-    dt = x.dtype
     x, h = _add_norm(x, r, lp.get("ln1"), cfg)
     q, k, v = _qkv(cfg, cos, sin, h, lp)
     if cfg.sink == "learned":
@@ -310,8 +309,7 @@ def _block(cfg: LMConfig, cos, sin, x, r, lp):
         sink = torch.full((H,), cfg.sink_init, dtype=F32, device=x.device)
     else:
         sink = None
-    a = _attention(q, k, v, sink, cfg)
-    a = a.transpose(1, 2).reshape(B, T, d)
+    a = heads_to_tokens(_attention(q, k, v, sink, cfg))
     x, h2 = _add_norm(x, a @ lp["w_o_c"], lp.get("ln2"), cfg)
     if cfg.ffn not in ("swiglu", "alu_glu"):
         raise ValueError(f"unknown ffn {cfg.ffn!r}")

@@ -10,7 +10,9 @@ functional signature of the reference, without copying 1.4 GB per step).
 The Newton-Schulz products run as batched GEMMs over the layer-stacked
 weights (hipBLASLt through torch). ``ns_dtype`` selects their input type:
 bfloat16 (default; the reference's float32 matmuls run as single bfloat16
-passes on its TPUs at default precision) or float32.
+passes on its TPUs at default precision) or float32. Every transpose the
+iteration needs is materialised by libalgx's tiled transpose kernel (one
+read and one write of the batch) rather than by a strided torch copy.
 """
 
 import math
@@ -18,7 +20,16 @@ from typing import Any, Callable, Dict, Optional, Tuple
 
 import torch
 
+from .layout import transpose_last2
+
 F32 = torch.float32
+
+
+def _mT(x: torch.Tensor) -> torch.Tensor:
+    """x.transpose(-2, -1), contiguous: libalgx's tiled transpose for device
+    tensors (torch's strided copy of the same moves runs 2-3x slower there);
+    tensors on the host take torch's copy."""
+    return transpose_last2(x) if x.is_cuda else x.transpose(-2, -1).contiguous()
 
 
 _NS_ABC = (3.4445, -4.7750, 2.0315)
@@ -37,7 +48,7 @@ def _ns_wide(X: torch.Tensor, steps: int, eps: float, ns_dtype: torch.dtype) -> 
     X = (X / norm).to(ns_dtype).contiguous()
 
     def gram(x):
-        return torch.bmm(x, x.transpose(-2, -1).contiguous())
+        return torch.bmm(x, _mT(x))
 
     for _ in range(steps):
         A = gram(X)
@@ -59,10 +70,10 @@ def newton_schulz_5(G: torch.Tensor, steps: int = 5, eps: float = 1e-7,
     M, N = G.shape[-2], G.shape[-1]
     X = G.reshape((-1, M, N))
     if M > N:
-        X = X.transpose(-2, -1)
+        X = _mT(X.to(F32))
     X = _ns_wide(X, steps, eps, ns_dtype)
     if M > N:
-        X = X.transpose(-2, -1)
+        X = _mT(X)
     return (X.to(F32) * math.sqrt(max(1.0, float(M) / float(N)))).reshape(G.shape)
 
 
@@ -76,7 +87,7 @@ def newton_schulz_many(Gs, steps: int = 5, eps: float = 1e-7,
         M, N = G.shape[-2], G.shape[-1]
         X = G.reshape((-1, M, N))
         if M > N:
-            X = X.transpose(-2, -1)
+            X = _mT(X.to(F32))
         groups.setdefault(tuple(X.shape[-2:]), []).append((i, X))
     out = [None] * len(Gs)
     for items in groups.values():
@@ -89,7 +100,7 @@ def newton_schulz_many(Gs, steps: int = 5, eps: float = 1e-7,
             G = Gs[i]
             M, N = G.shape[-2], G.shape[-1]
             if M > N:
-                y = y.transpose(-2, -1)
+                y = _mT(y)
             out[i] = (y.to(F32) * math.sqrt(max(1.0, float(M) / float(N)))).reshape(G.shape)
     return out
 

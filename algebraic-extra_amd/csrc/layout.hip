@@ -1,0 +1,114 @@
+// Layout changes of the model step that XLA folds into its fusions in the
+// reference and torch would run as strided element copies:
+//
+// * swap_axes: (B, P, Q, row) -> (B, Q, P, row) with rows moved whole, as
+//   16-byte vectors: the attention output's (B, H, T, D) -> (B, T, H*D) of
+//   model.py:182, and its inverse for the gradient.
+// * transpose: batched [K][M][N] -> [K][N][M] of 2- or 4-byte elements
+//   through a 64 x 64 LDS tile: the swapaxes of Muon's Newton-Schulz
+//   (optimizers.py:41, :49, :58, :62).
+//
+// Both are HBM-bound byte moves: every source byte is read once and every
+// destination byte written once, in 128-byte (or longer) runs per wave.
+#include "common.h"
+
+namespace algx {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTile = 64;
+
+// dst vector i = ((b * Q + q) * P + p) * vpr + c  <-  src ((b * P + p) * Q + q) * vpr + c.
+__global__ __launch_bounds__(kThreads) void swap_axes_kernel(const i32x4* __restrict__ src,
+                                                             i32x4* __restrict__ dst, uint32_t P,
+                                                             uint32_t Q, uint32_t vpr,
+                                                             uint32_t total) {
+  const uint32_t i = blockIdx.x * (uint32_t)kThreads + threadIdx.x;
+  if (i >= total) return;
+  const uint32_t c = i % vpr;
+  uint32_t r = i / vpr;
+  const uint32_t p = r % P;
+  r /= P;
+  const uint32_t q = r % Q, b = r / Q;
+  dst[i] = src[((b * P + p) * Q + q) * vpr + c];
+}
+
+// One 64 x 64 tile of one matrix: row-contiguous reads of the source (one
+// 64-element run per wave instruction) into LDS, row-contiguous writes of the
+// destination read down the LDS columns (row pitch 65 elements, so the 64
+// lanes of a column read fall in distinct banks).
+template <typename E>
+__global__ __launch_bounds__(kThreads) void transpose_kernel(const E* __restrict__ src,
+                                                             E* __restrict__ dst, int M, int N,
+                                                             int tiles_n) {
+  __shared__ E tile[kTile][kTile + 1];
+  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  const int m0 = tm * kTile, n0 = tn * kTile;
+  const int64_t base = (int64_t)blockIdx.y * M * N;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int r = w; r < kTile; r += kThreads / 64) {
+    const int m = m0 + r, n = n0 + lane;
+    if (m < M && n < N) tile[r][lane] = src[base + (int64_t)m * N + n];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = w; r < kTile; r += kThreads / 64) {
+    const int n = n0 + r, m = m0 + lane;
+    if (n < N && m < M) dst[base + (int64_t)n * M + m] = tile[lane][r];
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+bool overlaps(const void* a, const void* b, int64_t bytes) {
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + (uintptr_t)bytes && y < x + (uintptr_t)bytes;
+}
+
+}  // namespace
+}  // namespace algx
+
+using namespace algx;
+
+extern "C" int32_t algx_swap_axes(const void* src, void* dst, int64_t B, int64_t P, int64_t Q,
+                                  int64_t row_bytes, void* stream) {
+  if (B < 0 || P < 0 || Q < 0) return fail("swap_axes: negative extent");
+  if (row_bytes <= 0 || row_bytes % 16) return fail("swap_axes: row_bytes must be a positive multiple of 16");
+  const int64_t vpr = row_bytes / 16;
+  const int64_t total = B * P * Q * vpr;
+  if (total == 0) return 0;
+  if (total >= ((int64_t)1 << 32) - kThreads) return fail("swap_axes: more than 2^32 16-byte vectors");
+  if (src == nullptr || dst == nullptr) return fail("swap_axes: null pointer");
+  if (!aligned16(src) || !aligned16(dst)) return fail("swap_axes: pointers must be 16-byte aligned");
+  if (overlaps(src, dst, total * 16)) return fail("swap_axes: source and destination overlap");
+  const int64_t blocks = (total + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(swap_axes_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const i32x4*)src, (i32x4*)dst, (uint32_t)P,
+                     (uint32_t)Q, (uint32_t)vpr, (uint32_t)total);
+  return check_launch("swap_axes");
+}
+
+extern "C" int32_t algx_transpose(const void* src, void* dst, int64_t K, int64_t M, int64_t N,
+                                  int32_t elem_bytes, void* stream) {
+  if (K < 0 || M < 0 || N < 0) return fail("transpose: negative extent");
+  if (elem_bytes != 2 && elem_bytes != 4) return fail("transpose: elem_bytes must be 2 or 4");
+  if (K == 0 || M == 0 || N == 0) return 0;
+  if (K > 65535) return fail("transpose: at most 65535 matrices");
+  if (M >= ((int64_t)1 << 31) || N >= ((int64_t)1 << 31)) return fail("transpose: extent too large");
+  const int64_t tiles_n = (N + kTile - 1) / kTile;
+  const int64_t tiles = (M + kTile - 1) / kTile * tiles_n;
+  if (tiles >= ((int64_t)1 << 31)) return fail("transpose: too many tiles");
+  if (src == nullptr || dst == nullptr) return fail("transpose: null pointer");
+  if (overlaps(src, dst, K * M * N * elem_bytes)) return fail("transpose: source and destination overlap");
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((uint32_t)tiles, (uint32_t)K);
+  if (elem_bytes == 2)
+    hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, dim3(kThreads), 0, s,
+                       (const uint16_t*)src, (uint16_t*)dst, (int)M, (int)N, (int)tiles_n);
+  else
+    hipLaunchKernelGGL(transpose_kernel<uint32_t>, grid, dim3(kThreads), 0, s,
+                       (const uint32_t*)src, (uint32_t*)dst, (int)M, (int)N, (int)tiles_n);
+  return check_launch("transpose");
+}

@@ -163,7 +163,38 @@ def bench_head(steps, warmup, dev, N=16384, d=768, V=50304, kind="alg_ce", n=8, 
     flops = 3 * 2 * N * d * V
     return {"workload": f"N={N},d={d},V={V},{kind} n={n} c={c}", "ms_per_step": dt * 1e3,
             "tokens_per_s": N / dt, "tflops": flops / dt / 1e12,
-            "frac": flops / dt / 1e12 / PEAK_BF16_TFLOPS, **split}
+            "frac": flops / dt / 1e12 / PEAK_BF16_TFLOPS, **split,
+            "library_gemm_tflops": library_gemm_rates(h.detach(), E.detach())}
+
+
+def library_gemm_rates(h, E, iters=10):
+    """The rate torch's GEMM library (hipBLASLt / rocBLAS, default heuristics)
+    reaches on the head's three products as plain bf16 GEMMs: the logits
+    z = h E^T (written out, which the fused kernels never do), dh = dz E and
+    dE = dz^T h with a [N, V] dz. A ceiling reference for the head's own
+    MFMA loops at the same shapes, not part of the timed step."""
+    import torch
+    N, d = h.shape
+    V = E.shape[0]
+    dz = torch.empty((N, V), device=h.device, dtype=torch.bfloat16).normal_(0.0, 1e-3)
+    cases = {"logits": lambda: torch.mm(h, E.t()), "dh": lambda: torch.mm(dz, E),
+             "dE": lambda: torch.mm(dz.t(), h)}
+    flops = 2.0 * N * d * V
+    out = {}
+    for name, f in cases.items():
+        for _ in range(2):
+            f()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            f()
+        e.record()
+        torch.cuda.synchronize()
+        out[name] = round(flops / (s.elapsed_time(e) / iters * 1e-3) / 1e12, 1)
+    del dz
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_qknorm(steps, warmup, dev):
@@ -323,17 +354,22 @@ def traffic_bytes():
         return json.load(f).get("bytes_per_launch")
 
 
-def cpu_baseline(B, H, T, D, heads=None):
-    # The whole configs[1] workload, twice over (about 10 s on 16 host cores).
+def cpu_baseline(B, H, T, D, heads=None, runs=6):
+    # The whole configs[1] workload, twice over (about 10 s on 16 host cores),
+    # split into `runs` equal runs; the rate is the median run's.
     heads = heads or 2 * B * H
     from oracle.cpu_baseline import time_attention_fwd_bwd
-    secs, threads = time_attention_fwd_bwd(T=T, D=D, heads=heads)
+    times, threads = time_attention_fwd_bwd(T=T, D=D, heads=heads)
+    per_run = heads // runs
+    run_secs = sorted(sum(times[i * per_run:(i + 1) * per_run]) for i in range(runs))
+    med = 0.5 * (run_secs[(runs - 1) // 2] + run_secs[runs // 2])
     per_head = 3.5 * 4.0 * T * T * D / 2.0
-    return {"value": heads * per_head / secs / 1e12, "unit": "TFLOP/s", "cores": threads,
+    return {"value": per_run * per_head / med / 1e12, "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
-            "sample": f"{heads} (b,h)-head fwd+bwd passes ({heads / (B * H):g}x the configs[1] workload of {B * H} heads), dense "
-                      f"algebraic.asinh_attention fwd + autograd bwd in torch-CPU float32, "
-                      f"{secs:.1f} s"}
+            "sample": f"{heads} (b,h)-head fwd+bwd passes ({heads / (B * H):g}x the configs[1] "
+                      f"workload of {B * H} heads) in {runs} runs of {per_run}, median run "
+                      f"{med:.2f} s (all {sum(times):.1f} s); dense algebraic.asinh_attention "
+                      f"fwd + autograd bwd in torch-CPU float32"}
 
 
 def main():

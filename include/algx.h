@@ -239,6 +239,21 @@ int32_t algx_qk_prologue_bwd(const void* q, const void* k, const float* q_gain, 
                              int32_t B, int32_t T, int32_t H, int32_t D, int32_t dtype, float eps,
                              void* stream);
 
+/* ------------------------------------------------------------ layout moves
+ * Byte moves of the model step that the reference leaves to XLA.
+ * algx_swap_axes: dst (B, Q, P, row) = src (B, P, Q, row), rows of row_bytes
+ * bytes (a positive multiple of 16) moved whole; src and dst 16-byte aligned,
+ * not overlapping, fewer than 2^32 16-byte vectors. The attention output's
+ * a.transpose(0, 2, 1, 3).reshape(B, T, d) (src/algebraic/model.py:182) and,
+ * with P and Q exchanged, its gradient.
+ * algx_transpose: dst [K][N][M] = src [K][M][N] for elements of elem_bytes
+ * = 2 or 4 bytes, K <= 65535, not overlapping: the swapaxes(X, -2, -1) of the
+ * Newton-Schulz iteration (src/algebraic/optimizers.py:41, :49, :58, :62). */
+int32_t algx_swap_axes(const void* src, void* dst, int64_t B, int64_t P, int64_t Q,
+                       int64_t row_bytes, void* stream);
+int32_t algx_transpose(const void* src, void* dst, int64_t K, int64_t M, int64_t N,
+                       int32_t elem_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -44,12 +44,13 @@ def dense_asinh_attention(q, k, v, n, c, mask):
 
 
 def time_attention_fwd_bwd(T=2048, D=64, n=16, c=8.0, heads=8, threads=None, seed=0):
-    """Seconds for `heads` single-head forward+backward passes, and the thread count."""
+    """Seconds of each of `heads` single-head forward+backward passes (a
+    list), and the thread count."""
     threads = threads or os.cpu_count() or 1
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(seed)
     mask = torch.tril(torch.ones(T, T, dtype=torch.bool))
-    total = 0.0
+    times = []
     for _ in range(heads):
         q = torch.randn(T, D, generator=g)
         k = torch.randn(T, D, generator=g)
@@ -63,5 +64,5 @@ def time_attention_fwd_bwd(T=2048, D=64, n=16, c=8.0, heads=8, threads=None, see
         t0 = time.perf_counter()
         o = dense_asinh_attention(q, k, v, n, c, mask)
         torch.autograd.grad(o, (q, k, v), do)
-        total += time.perf_counter() - t0
-    return total, threads
+        times.append(time.perf_counter() - t0)
+    return times, threads

@@ -144,3 +144,29 @@ def test_elementwise_validation():
         alu_glu(_t((4, 64)), _t((4, 32)))
     with pytest.raises(ValueError, match="one dtype"):
         alu(_t((4, 64), torch.float64))
+
+
+def test_layout_validation_without_a_gpu():
+    """algx_swap_axes / algx_transpose reject bad arguments before any launch;
+    empty moves succeed without touching the device."""
+    lib = _lib.load()
+    g, h = ctypes.c_void_p(16), ctypes.c_void_p(1 << 20)
+    assert lib.algx_swap_axes(g, h, 2, 3, 4, 24, None) != 0
+    assert b"multiple of 16" in lib.algx_last_error()
+    assert lib.algx_swap_axes(ctypes.c_void_p(24), h, 2, 3, 4, 32, None) != 0
+    assert b"16-byte aligned" in lib.algx_last_error()
+    assert lib.algx_swap_axes(g, ctypes.c_void_p(48), 2, 3, 4, 32, None) != 0
+    assert b"overlap" in lib.algx_last_error()
+    assert lib.algx_swap_axes(None, None, 0, 3, 4, 32, None) == 0
+    assert lib.algx_transpose(g, h, 2, 3, 4, 8, None) != 0
+    assert b"elem_bytes" in lib.algx_last_error()
+    assert lib.algx_transpose(g, h, 70000, 3, 4, 2, None) != 0
+    assert b"65535" in lib.algx_last_error()
+    assert lib.algx_transpose(g, ctypes.c_void_p(20), 1, 3, 4, 2, None) != 0
+    assert b"overlap" in lib.algx_last_error()
+    assert lib.algx_transpose(None, None, 3, 0, 4, 2, None) == 0
+    from algebraic_amd.layout import heads_to_tokens, transpose_last2
+    with pytest.raises(ValueError, match="multiple of 16 bytes"):
+        heads_to_tokens(_t((1, 2, 3, 4)))
+    with pytest.raises(ValueError, match="2 or 4 bytes"):
+        transpose_last2(_t((3, 4), torch.float64))
