@@ -4,9 +4,11 @@
 // * swap_axes: (B, P, Q, row) -> (B, Q, P, row) with rows moved whole, as
 //   16-byte vectors: the attention output's (B, H, T, D) -> (B, T, H*D) of
 //   model.py:182, and its inverse for the gradient.
-// * transpose: batched [K][M][N] -> [K][N][M] of 2- or 4-byte elements
-//   through a 64 x 64 LDS tile: the swapaxes of Muon's Newton-Schulz
-//   (optimizers.py:41, :49, :58, :62).
+// * transpose: batched [K][M][N] -> [K][N][M] of 2- or 4-byte elements: the
+//   swapaxes of Muon's Newton-Schulz (optimizers.py:41, :49, :58, :62). With
+//   M and N multiples of the 16-byte vector (8 bf16 or 4 float32) every lane
+//   transposes one square block in registers (no LDS); other shapes go
+//   through a 64 x 64 LDS tile.
 //
 // Both are HBM-bound byte moves: every source byte is read once and every
 // destination byte written once, in 128-byte (or longer) runs per wave.
@@ -60,6 +62,49 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(const E* __restrict
   }
 }
 
+// One wave per 64 x 64 (bf16) or 32 x 32 (float32) tile; lane (i, j) =
+// (lane / 8, lane % 8) owns the square block of V x V elements (V = 16 bytes /
+// element size) at rows V i, columns V j of the tile: V 16-byte row loads,
+// the block transposed in registers, V 16-byte row stores. Each load or store
+// instruction moves 8 runs of 128 contiguous bytes.
+template <int V>
+__global__ __launch_bounds__(kThreads) void transpose_block_kernel(const i32x4* __restrict__ src,
+                                                                   i32x4* __restrict__ dst,
+                                                                   int M, int N, int tiles_n,
+                                                                   int tiles) {
+  constexpr int T = 8 * V;  // tile edge in elements
+  const int lane = threadIdx.x & 63;
+  const int tile = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (tile >= tiles) return;
+  const int m0 = (tile / tiles_n) * T + V * (lane >> 3);
+  const int n0 = (tile % tiles_n) * T + V * (lane & 7);
+  if (m0 >= M || n0 >= N) return;
+  // In 16-byte vectors: a row of the source holds N / V, of the destination M / V.
+  const int64_t base = (int64_t)blockIdx.y * M * (N / V);
+  const int64_t nv = N / V, mv = M / V;
+  i32x4 in[V];
+#pragma unroll
+  for (int r = 0; r < V; ++r) in[r] = src[base + (int64_t)(m0 + r) * nv + n0 / V];
+  i32x4 out[V];
+  if (V == 8) {
+    // bf16: out row c, word k = (element c of row 2k) | (element c of row 2k+1) << 16.
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t a = (uint32_t)in[2 * k][c >> 1], b = (uint32_t)in[2 * k + 1][c >> 1];
+        out[c][k] = (int)((c & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16)));
+      }
+  } else {
+#pragma unroll
+    for (int c = 0; c < V; ++c)
+#pragma unroll
+      for (int k = 0; k < V; ++k) out[c][k] = in[k][c];
+  }
+#pragma unroll
+  for (int c = 0; c < V; ++c) dst[base + (int64_t)(n0 + c) * mv + m0 / V] = out[c];
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 bool overlaps(const void* a, const void* b, int64_t bytes) {
@@ -103,6 +148,19 @@ extern "C" int32_t algx_transpose(const void* src, void* dst, int64_t K, int64_t
   if (src == nullptr || dst == nullptr) return fail("transpose: null pointer");
   if (overlaps(src, dst, K * M * N * elem_bytes)) return fail("transpose: source and destination overlap");
   hipStream_t s = (hipStream_t)stream;
+  const int V = 16 / elem_bytes;
+  const int64_t bt_n = (N + 8 * V - 1) / (8 * V);
+  const int64_t bt = (M + 8 * V - 1) / (8 * V) * bt_n;
+  if (M % V == 0 && N % V == 0 && aligned16(src) && aligned16(dst) && bt < ((int64_t)1 << 31)) {
+    const dim3 bgrid((uint32_t)((bt + kThreads / 64 - 1) / (kThreads / 64)), (uint32_t)K);
+    if (V == 8)
+      hipLaunchKernelGGL(transpose_block_kernel<8>, bgrid, dim3(kThreads), 0, s,
+                         (const i32x4*)src, (i32x4*)dst, (int)M, (int)N, (int)bt_n, (int)bt);
+    else
+      hipLaunchKernelGGL(transpose_block_kernel<4>, bgrid, dim3(kThreads), 0, s,
+                         (const i32x4*)src, (i32x4*)dst, (int)M, (int)N, (int)bt_n, (int)bt);
+    return check_launch("transpose");
+  }
   const dim3 grid((uint32_t)tiles, (uint32_t)K);
   if (elem_bytes == 2)
     hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, dim3(kThreads), 0, s,

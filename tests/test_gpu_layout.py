@@ -5,7 +5,9 @@ permutation of the same tensor: heads_to_tokens against
 ``a.transpose(1, 2).reshape(B, T, H * D)`` (the reference's
 ``a.transpose(0, 2, 1, 3).reshape(B, T, d)``, model.py:182) and
 transpose_last2 against ``x.transpose(-2, -1)`` (optimizers.py:41, :49), with
-ragged shapes that leave partial 64 x 64 tiles, and their gradients.
+ragged shapes that leave partial tiles on both of its paths (register blocks
+when both extents are multiples of 16 bytes, LDS tiles otherwise), and their
+gradients.
 """
 
 import pytest
@@ -57,6 +59,9 @@ def test_heads_to_tokens_noncontiguous_input():
     ((1, 1, 1), torch.bfloat16),
     ((7, 1), torch.float32),
     ((4, 2, 3, 100, 70), torch.bfloat16),
+    ((3, 72, 40), torch.bfloat16),
+    ((2, 36, 20), torch.float32),
+    ((1, 8, 8), torch.bfloat16),
 ])
 def test_transpose_matches_torch(shape, dtype):
     x = _rand(shape, dtype, 21).requires_grad_(True)
