@@ -12,7 +12,10 @@ weights (hipBLASLt through torch). ``ns_dtype`` selects their input type:
 bfloat16 (default; the reference's float32 matmuls run as single bfloat16
 passes on its TPUs at default precision) or float32. Every transpose the
 iteration needs is materialised by libalgx's tiled transpose kernel (one
-read and one write of the batch) rather than by a strided torch copy.
+read and one write of the batch) rather than by a strided torch copy, and
+Muon's elementwise steps around it (momentum with the Nesterov look-ahead,
+and the decayed update from the orthogonalised matrix) are single libalgx
+passes over the float32 state.
 """
 
 import math
@@ -20,6 +23,7 @@ from typing import Any, Callable, Dict, Optional, Tuple
 
 import torch
 
+from . import _lib
 from .layout import transpose_last2
 
 F32 = torch.float32
@@ -30,6 +34,37 @@ def _mT(x: torch.Tensor) -> torch.Tensor:
     tensors (torch's strided copy of the same moves runs 2-3x slower there);
     tensors on the host take torch's copy."""
     return transpose_last2(x) if x.is_cuda else x.transpose(-2, -1).contiguous()
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _muon_momentum(g: torch.Tensor, m: torch.Tensor, mu: float) -> torch.Tensor:
+    """m <- mu m + (1 - mu) g in place; returns the look-ahead (1 - mu) g + mu m
+    (optimizers.py:200-201). Device tensors: one libalgx pass."""
+    if m.is_cuda:
+        g = _aligned(g)
+        look = torch.empty_like(m)
+        _lib.call("algx_muon_momentum", _lib.ptr(g), _lib.ptr(m), _lib.ptr(look), m.numel(),
+                  float(mu), _lib.stream())
+        return look
+    m.mul_(mu).add_(g, alpha=1.0 - mu)
+    return g.mul(1.0 - mu).add_(m, alpha=mu)
+
+
+def _muon_apply(p: torch.Tensor, o: torch.Tensor, decay_fac: float, step: float) -> None:
+    """p <- p * decay_fac - step * o in place (optimizers.py:203-204), o in the
+    Newton-Schulz dtype. Device tensors: one libalgx pass."""
+    if p.is_cuda:
+        o = _aligned(o)
+        _lib.call("algx_muon_apply", _lib.ptr(p), _lib.ptr(o), p.numel(),
+                  _lib.dtype_code(o.dtype), float(decay_fac), float(step), _lib.stream())
+        return
+    if decay_fac != 1.0:
+        p.mul_(decay_fac)
+    p.add_(o.to(F32), alpha=-step)
 
 
 _NS_ABC = (3.4445, -4.7750, 2.0315)
@@ -82,6 +117,14 @@ def newton_schulz_many(Gs, steps: int = 5, eps: float = 1e-7,
     """newton_schulz_5 of every tensor in Gs, the matrices of equal (oriented)
     shape run as one batch: the model's 7 stacked weights become two batches
     ([w_q | w_k | w_v | w_o] and [w_g | w_u | w_d^T])."""
+    return [(y.to(F32) * sc).reshape(G.shape)
+            for G, (y, sc) in zip(Gs, _newton_schulz_unscaled(Gs, steps, eps, ns_dtype))]
+
+
+def _newton_schulz_unscaled(Gs, steps, eps, ns_dtype):
+    """(X, scale) per tensor of Gs: X the orthogonalised matrix in ns_dtype
+    and G's layout, scale the aspect factor sqrt(max(1, M / N)) still to be
+    applied (optimizers.py:63-64)."""
     groups: Dict[Tuple[int, int], list] = {}
     for i, G in enumerate(Gs):
         M, N = G.shape[-2], G.shape[-1]
@@ -101,7 +144,7 @@ def newton_schulz_many(Gs, steps: int = 5, eps: float = 1e-7,
             M, N = G.shape[-2], G.shape[-1]
             if M > N:
                 y = _mT(y)
-            out[i] = (y.to(F32) * math.sqrt(max(1.0, float(M) / float(N)))).reshape(G.shape)
+            out[i] = (y.reshape(G.shape), math.sqrt(max(1.0, float(M) / float(N))))
     return out
 
 
@@ -203,9 +246,8 @@ def get_optimizer(name: str, lr: float, weight_decay: float = 0.1, total_steps: 
             m, v = opt_state.m[path], opt_state.v[path]
             decay = bool(_get(decay_mask, path))
             if uses_muon and is_muon_param(path, p):
-                # m <- mu m + (1 - mu) g; Nesterov look-ahead; orthogonalised below
-                m.mul_(muon_momentum).add_(g, alpha=1.0 - muon_momentum)
-                muon_jobs.append((p, decay, g.mul(1.0 - muon_momentum).add_(m, alpha=muon_momentum)))
+                # m <- mu m + (1 - mu) g and the Nesterov look-ahead, orthogonalised below
+                muon_jobs.append((p, decay, _muon_momentum(g, m, muon_momentum)))
                 continue
             m.mul_(b1).add_(g, alpha=1.0 - b1)
             v.mul_(b2).addcmul_(g, g, value=1.0 - b2)
@@ -217,12 +259,10 @@ def get_optimizer(name: str, lr: float, weight_decay: float = 0.1, total_steps: 
                 p.mul_(1.0 - adam_lr * weight_decay)
             p.add_(u, alpha=-adam_lr)
         if muon_jobs:
-            ortho = newton_schulz_many([look for _, _, look in muon_jobs], steps=muon_steps,
-                                       ns_dtype=ns_dtype)
-            for (p, decay, _), o in zip(muon_jobs, ortho):
-                if decay:
-                    p.mul_(1.0 - muon_lr_t * m_wd)
-                p.add_(o, alpha=-muon_lr_t)
+            ortho = _newton_schulz_unscaled([look for _, _, look in muon_jobs], muon_steps, 1e-7,
+                                            ns_dtype)
+            for (p, decay, _), (o, sc) in zip(muon_jobs, ortho):
+                _muon_apply(p, o, 1.0 - muon_lr_t * m_wd if decay else 1.0, muon_lr_t * sc)
         opt_state.count += 1
         return params, opt_state
 

@@ -254,6 +254,20 @@ int32_t algx_swap_axes(const void* src, void* dst, int64_t B, int64_t P, int64_t
 int32_t algx_transpose(const void* src, void* dst, int64_t K, int64_t M, int64_t N,
                        int32_t elem_bytes, void* stream);
 
+/* ------------------------------------------------------------- Muon steps
+ * The elementwise parts of Muon's update (src/algebraic/optimizers.py:200-204)
+ * over n float32 elements (pointers 16-byte aligned):
+ * algx_muon_momentum: m <- mu m + (1 - mu) g; look = (1 - mu) g + mu m
+ *   (:200-201), look being the matrix newton_schulz_5 orthogonalises (:202).
+ * algx_muon_apply: p <- p * decay - step * o (:203-204), o the
+ *   orthogonalised update in bf16 (8-byte aligned) or float32 (o_dtype),
+ *   decay = 1 - lr * wd for decayed leaves (else 1), step = lr times the
+ *   aspect factor sqrt(max(1, M / N)) of newton_schulz_5 (:63). */
+int32_t algx_muon_momentum(const float* g, float* m, float* look, int64_t n, float mu,
+                           void* stream);
+int32_t algx_muon_apply(float* p, const void* o, int64_t n, int32_t o_dtype, float decay,
+                        float step, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

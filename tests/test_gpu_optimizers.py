@@ -60,3 +60,28 @@ def test_muon_adamw_step_on_gpu_matches_oracle():
             tol = 3e-2 if muon[k] else 2e-3
             assert rel_l2(got[k] - p0[k], flat[k] - p0[k]) <= tol, k
         flat = got
+
+
+@pytest.mark.parametrize("n", [0, 1, 7, 4096, 1000003])
+def test_muon_elementwise_kernels(n):
+    """algx_muon_momentum / algx_muon_apply against optimizers.py:200-204 in
+    float64 (float32 state: a few ulp), with n not a multiple of the 4-element
+    vector and o in bf16 and float32."""
+    rng = np.random.default_rng(n)
+    g64, m64, p64 = (rng.standard_normal(n) for _ in range(3))
+    g = torch.tensor(g64, dtype=torch.float32, device=DEV)
+    m = torch.tensor(m64, dtype=torch.float32, device=DEV)
+    mu = 0.95
+    look = O._muon_momentum(g, m, mu)
+    gf, mf = g64.astype(np.float32).astype(np.float64), m64.astype(np.float32).astype(np.float64)
+    m_want = mu * mf + (1 - mu) * gf
+    look_want = (1 - mu) * gf + mu * m_want
+    np.testing.assert_allclose(m.double().cpu().numpy(), m_want, rtol=0, atol=1e-6)
+    np.testing.assert_allclose(look.double().cpu().numpy(), look_want, rtol=0, atol=1e-6)
+    for odt in (torch.bfloat16, torch.float32):
+        p = torch.tensor(p64, dtype=torch.float32, device=DEV)
+        o = look.to(odt)
+        decay, step = 1.0 - 2e-3 * 0.1, 2e-3 * 1.62
+        O._muon_apply(p, o, decay, step)
+        want = p64.astype(np.float32).astype(np.float64) * decay - step * o.double().cpu().numpy()
+        np.testing.assert_allclose(p.double().cpu().numpy(), want, rtol=0, atol=2e-6)
