@@ -43,9 +43,10 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
 
 def _muon_momentum(g: torch.Tensor, m: torch.Tensor, mu: float) -> torch.Tensor:
     """m <- mu m + (1 - mu) g in place; returns the look-ahead (1 - mu) g + mu m
-    (optimizers.py:200-201). Device tensors: one libalgx pass."""
-    if m.is_cuda:
-        g = _aligned(g)
+    (optimizers.py:200-201). Contiguous float32 device state: one libalgx
+    pass."""
+    if m.is_cuda and m.dtype == F32 and m.is_contiguous() and m.data_ptr() % 16 == 0:
+        g = _aligned(g.to(F32))
         look = torch.empty_like(m)
         _lib.call("algx_muon_momentum", _lib.ptr(g), _lib.ptr(m), _lib.ptr(look), m.numel(),
                   float(mu), _lib.stream())
@@ -56,8 +57,9 @@ def _muon_momentum(g: torch.Tensor, m: torch.Tensor, mu: float) -> torch.Tensor:
 
 def _muon_apply(p: torch.Tensor, o: torch.Tensor, decay_fac: float, step: float) -> None:
     """p <- p * decay_fac - step * o in place (optimizers.py:203-204), o in the
-    Newton-Schulz dtype. Device tensors: one libalgx pass."""
-    if p.is_cuda:
+    Newton-Schulz dtype. Contiguous float32 device parameters: one libalgx
+    pass."""
+    if p.is_cuda and p.dtype == F32 and p.is_contiguous() and p.data_ptr() % 16 == 0:
         o = _aligned(o)
         _lib.call("algx_muon_apply", _lib.ptr(p), _lib.ptr(o), p.numel(),
                   _lib.dtype_code(o.dtype), float(decay_fac), float(step), _lib.stream())
