@@ -72,17 +72,38 @@ def _muon_apply(p: torch.Tensor, o: torch.Tensor, decay_fac: float, step: float)
 _NS_ABC = (3.4445, -4.7750, 2.0315)
 
 
+def _normalize_into(X: torch.Tensor, out: torch.Tensor, eps: float) -> None:
+    """out <- X / sqrt(sum(X^2) + eps) per (m, n) matrix of X (k, m, n), cast to
+    out's dtype (optimizers.py:44-45). Device tensors: two libalgx passes
+    (per-matrix sums of squares, then the scaled copy) with no float32
+    intermediate."""
+    X = X.to(F32).contiguous()
+    if X.is_cuda and out.is_contiguous() and out.dtype in (torch.bfloat16, F32):
+        K, MN = X.shape[0], X.shape[1] * X.shape[2]
+        ws = torch.empty(max(1, _lib.query("algx_ns_normalize_workspace_bytes", K, MN)),
+                         dtype=torch.uint8, device=X.device)
+        _lib.call("algx_ns_normalize", _lib.ptr(X), _lib.ptr(out), K, MN,
+                  _lib.dtype_code(out.dtype), float(eps), _lib.ptr(ws), _lib.stream())
+        return
+    norm = torch.sqrt((X * X).sum(dim=(-2, -1), keepdim=True) + eps)
+    out.copy_(X / norm)
+
+
 def _ns_wide(X: torch.Tensor, steps: int, eps: float, ns_dtype: torch.dtype) -> torch.Tensor:
-    """Newton-Schulz on a batch (k, m, n), m <= n, without the aspect factor.
+    """Newton-Schulz on a batch (k, m, n), m <= n, without the aspect factor."""
+    Xn = torch.empty(X.shape, dtype=ns_dtype, device=X.device)
+    _normalize_into(X, Xn, eps)
+    return _ns_iterate(Xn, steps)
+
+
+def _ns_iterate(X: torch.Tensor, steps: int) -> torch.Tensor:
+    """The iteration on a normalised, contiguous batch (k, m, n), m <= n.
 
     Each update is one batched GEMM with its linear combination folded into
     the GEMM's own alpha/beta: B = b A + c A A and X <- a X + B X
     (= baddbmm(X, B, X, beta=a)), X <- 1.5 X - 0.5 (X X^T) X for the
     refinements; only X X^T needs X^T materialised."""
     a, b, c = _NS_ABC
-    X = X.to(F32)
-    norm = torch.sqrt((X * X).sum(dim=(-2, -1), keepdim=True) + eps)
-    X = (X / norm).to(ns_dtype).contiguous()
 
     def gram(x):
         return torch.bmm(x, _mT(x))
@@ -136,8 +157,15 @@ def _newton_schulz_unscaled(Gs, steps, eps, ns_dtype):
         groups.setdefault(tuple(X.shape[-2:]), []).append((i, X))
     out = [None] * len(Gs)
     for items in groups.values():
-        batch = torch.cat([x for _, x in items], dim=0)
-        Y = _ns_wide(batch, steps, eps, ns_dtype)
+        # each matrix normalised straight into its slice of the batch
+        k_all = sum(x.shape[0] for _, x in items)
+        m, n = items[0][1].shape[-2:]
+        batch = torch.empty((k_all, m, n), dtype=ns_dtype, device=items[0][1].device)
+        k0 = 0
+        for _, x in items:
+            _normalize_into(x, batch[k0:k0 + x.shape[0]], eps)
+            k0 += x.shape[0]
+        Y = _ns_iterate(batch, steps)
         k0 = 0
         for i, x in items:
             y = Y[k0:k0 + x.shape[0]]

@@ -8,9 +8,13 @@
 // * apply: p <- p * decay - step * o for the orthogonalised update o (bf16 or
 //   float32), step = lr times the aspect factor of newton_schulz_5. Reads p,
 //   o; writes p.
+// * ns_normalize: X / sqrt(sum(X^2) + eps) per matrix, cast to the
+//   Newton-Schulz input type (optimizers.py:44-45): per-block sums of squares
+//   of each matrix, then one pass that reduces its matrix's partials (fixed
+//   order, so every block forms the same norm) and writes the scaled copy.
 //
-// Each thread owns 4 consecutive elements (one 16-byte float32 vector); the
-// last partial vector is done element by element.
+// momentum / apply: each thread owns 4 consecutive elements (one 16-byte
+// float32 vector); the last partial vector is done element by element.
 #include "common.h"
 
 namespace algx {
@@ -72,7 +76,95 @@ __global__ __launch_bounds__(kThreads) void muon_apply_kernel(float* __restrict_
   }
 }
 
+constexpr int kMaxNormBlocks = 256;  // partial sums per matrix
+
+// Block (b, k): sum of squares of elements [b * span, (b + 1) * span) of
+// matrix k, a fixed-order tree over the block's threads. VEC: 16-byte loads
+// (mn and span multiples of 4, x 16-byte aligned).
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void ns_sumsq_kernel(const float* __restrict__ x,
+                                                            float* __restrict__ partial,
+                                                            int64_t mn, int64_t span) {
+  const int64_t k = blockIdx.y;
+  const float* xk = x + k * mn;
+  const int64_t lo = blockIdx.x * span;
+  const int64_t hi = min(mn, lo + span);
+  float s0 = 0.0f, s1 = 0.0f;
+  if (VEC) {
+    for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 4 * kThreads) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(xk + i);
+      s0 = __builtin_fmaf(v[0], v[0], s0);
+      s1 = __builtin_fmaf(v[1], v[1], s1);
+      s0 = __builtin_fmaf(v[2], v[2], s0);
+      s1 = __builtin_fmaf(v[3], v[3], s1);
+    }
+  } else {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) s0 = __builtin_fmaf(xk[i], xk[i], s0);
+  }
+  __shared__ float red[kThreads];
+  red[threadIdx.x] = s0 + s1;
+  __syncthreads();
+#pragma unroll
+  for (int w = kThreads / 2; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) partial[k * gridDim.x + blockIdx.x] = red[0];
+}
+
+// Block (b, k): norm of matrix k from its nb partials (the same fixed-order
+// tree in every block of the matrix), then out = x / norm over the block's
+// span, cast to T. VEC: 16-byte loads and 4-element stores.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kThreads) void ns_scale_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ partial,
+                                                            int nb, T* __restrict__ out,
+                                                            int64_t mn, int64_t span, float eps) {
+  const int64_t k = blockIdx.y;
+  __shared__ float red[kMaxNormBlocks];
+  red[threadIdx.x] = threadIdx.x < nb ? partial[k * nb + threadIdx.x] : 0.0f;
+  __syncthreads();
+#pragma unroll
+  for (int w = kMaxNormBlocks / 2; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  const float norm = __builtin_sqrtf(red[0] + eps);
+  const float* xk = x + k * mn;
+  T* ok = out + k * mn;
+  const int64_t lo = blockIdx.x * span;
+  const int64_t hi = min(mn, lo + span);
+  if (VEC) {
+    for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 4 * kThreads) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(xk + i);
+      if (sizeof(T) == 2) {
+        bf16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = (bf16)(v[e] / norm);
+        *reinterpret_cast<bf16x4*>(ok + i) = o;
+      } else {
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = v[e] / norm;
+        *reinterpret_cast<f32x4*>(ok + i) = o;
+      }
+    }
+  } else {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) ok[i] = from_f<T>(xk[i] / norm);
+  }
+}
+
 int64_t blocks_of(int64_t n) { return (n + 4 * kThreads - 1) / (4 * kThreads); }
+
+// Blocks per matrix of the normalisation: ~2048 blocks over the batch, at
+// most kMaxNormBlocks per matrix and at least 4096 elements per block.
+int norm_blocks(int64_t K, int64_t mn) {
+  int64_t nb = (2048 + K - 1) / K;
+  const int64_t cap = (mn + 4095) / 4096;
+  if (nb > cap) nb = cap;
+  if (nb > kMaxNormBlocks) nb = kMaxNormBlocks;
+  return (int)(nb < 1 ? 1 : nb);
+}
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -111,4 +203,50 @@ extern "C" int32_t algx_muon_apply(float* p, const void* o, int64_t n, int32_t o
     hipLaunchKernelGGL(muon_apply_kernel<float>, dim3((uint32_t)blocks_of(n)), dim3(kThreads), 0,
                        s, p, (const float*)o, n, decay, step);
   return check_launch("muon_apply");
+}
+
+extern "C" int64_t algx_ns_normalize_workspace_bytes(int64_t K, int64_t MN) {
+  if (K <= 0 || MN <= 0) return 0;
+  return K * norm_blocks(K, MN) * (int64_t)sizeof(float);
+}
+
+extern "C" int32_t algx_ns_normalize(const float* x, void* out, int64_t K, int64_t MN,
+                                     int32_t out_dtype, float eps, void* workspace,
+                                     void* stream) {
+  if (K < 0 || MN < 0) return fail("ns_normalize: negative size");
+  if (out_dtype != ALGX_BF16 && out_dtype != ALGX_F32)
+    return fail("ns_normalize: out must be bf16 or f32");
+  if (!(eps >= 0.0f)) return fail("ns_normalize: eps must be non-negative");
+  if (K == 0 || MN == 0) return 0;
+  if (K > 65535) return fail("ns_normalize: at most 65535 matrices");
+  if (x == nullptr || out == nullptr || workspace == nullptr) return fail("ns_normalize: null pointer");
+  const int nb = norm_blocks(K, MN);
+  const bool vec = MN % 4 == 0 && aligned16(x) && ((uintptr_t)out & (out_dtype == ALGX_BF16 ? 7 : 15)) == 0;
+  int64_t span = (MN + nb - 1) / nb;
+  if (vec) span = (span + 3) / 4 * 4;
+  hipStream_t s = (hipStream_t)stream;
+  float* partial = (float*)workspace;
+  const dim3 grid((uint32_t)nb, (uint32_t)K);
+  if (vec)
+    hipLaunchKernelGGL(ns_sumsq_kernel<true>, grid, dim3(kThreads), 0, s, x, partial, MN, span);
+  else
+    hipLaunchKernelGGL(ns_sumsq_kernel<false>, grid, dim3(kThreads), 0, s, x, partial, MN, span);
+  if (int32_t rc = check_launch("ns_sumsq")) return rc;
+  static_assert(kMaxNormBlocks == kThreads, "one partial per thread in the norm reduction");
+  if (out_dtype == ALGX_BF16) {
+    if (vec)
+      hipLaunchKernelGGL((ns_scale_kernel<bf16, true>), grid, dim3(kThreads), 0, s, x, partial, nb,
+                         (bf16*)out, MN, span, eps);
+    else
+      hipLaunchKernelGGL((ns_scale_kernel<bf16, false>), grid, dim3(kThreads), 0, s, x, partial, nb,
+                         (bf16*)out, MN, span, eps);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((ns_scale_kernel<float, true>), grid, dim3(kThreads), 0, s, x, partial, nb,
+                         (float*)out, MN, span, eps);
+    else
+      hipLaunchKernelGGL((ns_scale_kernel<float, false>), grid, dim3(kThreads), 0, s, x, partial, nb,
+                         (float*)out, MN, span, eps);
+  }
+  return check_launch("ns_scale");
 }

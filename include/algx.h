@@ -267,6 +267,13 @@ int32_t algx_muon_momentum(const float* g, float* m, float* look, int64_t n, flo
                            void* stream);
 int32_t algx_muon_apply(float* p, const void* o, int64_t n, int32_t o_dtype, float decay,
                         float step, void* stream);
+/* algx_ns_normalize: out[k] = cast(x[k] / sqrt(sum(x[k]^2) + eps)) for K float32
+ * matrices of MN elements (newton_schulz_5's pre-normalisation,
+ * src/algebraic/optimizers.py:44-45), out in bf16 or float32 (out_dtype),
+ * K <= 65535; the workspace holds per-block partial sums (size from the query). */
+int64_t algx_ns_normalize_workspace_bytes(int64_t K, int64_t MN);
+int32_t algx_ns_normalize(const float* x, void* out, int64_t K, int64_t MN, int32_t out_dtype,
+                          float eps, void* workspace, void* stream);
 
 #ifdef __cplusplus
 }

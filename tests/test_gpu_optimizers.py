@@ -85,3 +85,20 @@ def test_muon_elementwise_kernels(n):
         O._muon_apply(p, o, decay, step)
         want = p64.astype(np.float32).astype(np.float64) * decay - step * o.double().cpu().numpy()
         np.testing.assert_allclose(p.double().cpu().numpy(), want, rtol=0, atol=2e-6)
+
+
+@pytest.mark.parametrize("shape", [(3, 5, 7), (2, 64, 96), (96, 1024, 1024), (1, 1, 3)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_ns_normalize_kernel(shape, out_dtype):
+    """algx_ns_normalize against optimizers.py:44-45 in float64: X / sqrt(sum
+    X^2 + eps) per matrix, on the vector path (extents a multiple of 4) and
+    the scalar one, written in bf16 (within one bf16 rounding) or float32."""
+    g = torch.Generator(device=DEV).manual_seed(sum(shape))
+    X = torch.randn(shape, generator=g, device=DEV) * 3.0
+    out = torch.empty(shape, dtype=out_dtype, device=DEV)
+    O._normalize_into(X, out, 1e-7)
+    x64 = X.double().cpu()
+    want = x64 / torch.sqrt((x64 * x64).sum(dim=(-2, -1), keepdim=True) + 1e-7)
+    got = out.double().cpu()
+    tol = 2.0 ** -8 if out_dtype == torch.bfloat16 else 4e-6
+    assert float(((got - want).abs() / want.abs().clamp_min(1e-30)).max()) <= tol

@@ -87,6 +87,22 @@ def test_fused_head_matches_oracle(kind, n, c, V):
         assert cos > 0.999
 
 
+@pytest.mark.parametrize("N,d,V", [(300, 64, 1000), (600, 40, 257), (8, 128, 300)])
+def test_fused_head_ragged_tiles(N, d, V):
+    """Token counts and vocabularies that leave partial 256-token and
+    vocabulary tiles, and a hidden width that is not a multiple of the 32-wide
+    k stage (block_n = N, so the reference's divisibility check holds)."""
+    h, e, t = _head_inputs(N, d, V, 5, 0.2)
+    for kind, n, c in (("alg_ce", 8, 2.0), ("ce", 16, 16.0)):
+        got = _head_run(h, e, t, kind=kind, n=n, c=c, block_n=N)
+        (obj, tel), (dh, de) = OH.fused_head(to_np(h), to_np(e), to_np(t), kind=kind, n=n, c=c,
+                                             dtype="bf16", g_obj=1.0)
+        assert abs(got[0] - obj) <= 2e-4 + 2e-3 * abs(obj)
+        np.testing.assert_allclose(got[1], tel, rtol=2e-2, atol=2e-4)
+        assert_bf16(got[2], dh, what="dh")
+        assert rel_l2(got[3], de) <= 1e-2
+
+
 @pytest.mark.parametrize("width", [768, 1024])
 def test_production_head_tiles_at_model_widths(width):
     """test_fused_head_tpu.py:43-67: 256 tokens, V=32768, E ~ 0.02 N(0,1), n=8, c=2."""
