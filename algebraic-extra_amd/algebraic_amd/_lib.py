@@ -69,6 +69,8 @@ SIGNATURES = {
     "algx_glu_packed_bwd": (_i32, [_p, _p, _p, _i64, _i32, _i32, _i32, _f32, _p]),
     "algx_swap_axes": (_i32, [_p, _p, _i64, _i64, _i64, _i64, _p]),
     "algx_transpose": (_i32, [_p, _p, _i64, _i64, _i64, _i32, _p]),
+    "algx_concat_cast": (_i32, [_p, _p, _i32, _p, _i64, _i32, _p]),
+    "algx_split_cast": (_i32, [_p, _p, _p, _i32, _i64, _i32, _p]),
     "algx_muon_momentum": (_i32, [_p, _p, _p, _i64, _f32, _p]),
     "algx_muon_apply": (_i32, [_p, _p, _i64, _i32, _f32, _f32, _p]),
     "algx_ns_normalize_workspace_bytes": (_i64, [_i64, _i64]),

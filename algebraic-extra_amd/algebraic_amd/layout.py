@@ -6,12 +6,20 @@ values moved whole; its gradient takes the inverse move.
 
 ``transpose_last2(x)``: (..., M, N) -> (..., N, M) contiguous, the
 ``swapaxes(X, -2, -1)`` of the Newton-Schulz iteration (optimizers.py:41,
-:49, :58, :62), through LDS tiles.
+:49, :58, :62): square blocks transposed in registers, or LDS tiles for
+extents that are not multiples of 16 bytes.
 
-Both accept any dtype whose rows (heads_to_tokens: D elements) span a multiple
-of 16 bytes (transpose_last2: 2- or 4-byte elements) and return new
+``concat_cast(parts, dtype)``: float32 tensors (..., C_i) joined along the
+last axis and cast to ``dtype`` (bf16 or float32) in one pass; the gradient
+is split and cast back to float32 in one pass. The model's per-step
+compute-dtype copies of the stacked weights for its fused projections.
+
+The first two accept any dtype whose rows (heads_to_tokens: D elements) span a
+multiple of 16 bytes (transpose_last2: 2- or 4-byte elements); all return new
 contiguous tensors.
 """
+
+import ctypes
 
 import torch
 
@@ -83,4 +91,48 @@ def transpose_last2(x: torch.Tensor) -> torch.Tensor:
     return _TransposeLast2.apply(x)
 
 
-__all__ = ["heads_to_tokens", "transpose_last2"]
+def _part_args(ts):
+    arr = (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+    cols = (ctypes.c_int64 * len(ts))(*[t.shape[-1] for t in ts])
+    return ctypes.cast(arr, ctypes.c_void_p), ctypes.cast(cols, ctypes.c_void_p), arr, cols
+
+
+class _ConcatCast(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, dtype, *parts):
+        parts = [_contig16(p) for p in parts]
+        lead = parts[0].shape[:-1]
+        rows = parts[0].numel() // parts[0].shape[-1]
+        out = torch.empty(lead + (sum(p.shape[-1] for p in parts),), dtype=dtype,
+                          device=parts[0].device)
+        pp, cc, keep_a, keep_c = _part_args(parts)
+        _lib.call("algx_concat_cast", pp, cc, len(parts), _lib.ptr(out), rows,
+                  _lib.dtype_code(dtype), _lib.stream())
+        ctx.shapes = [p.shape for p in parts]
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        g = _contig16(g)
+        grads = [torch.empty(sh, dtype=torch.float32, device=g.device) for sh in ctx.shapes]
+        rows = grads[0].numel() // grads[0].shape[-1]
+        pp, cc, keep_a, keep_c = _part_args(grads)
+        _lib.call("algx_split_cast", _lib.ptr(g), pp, cc, len(grads), rows,
+                  _lib.dtype_code(g.dtype), _lib.stream())
+        return (None, *grads)
+
+
+def concat_cast(parts, dtype: torch.dtype) -> torch.Tensor:
+    """torch.cat(parts, -1).to(dtype) for float32 parts of one leading shape
+    (last extents multiples of 4, at most 4 parts), as one pass each way."""
+    parts = list(parts)
+    if not 1 <= len(parts) <= 4:
+        raise ValueError("concat_cast joins 1 to 4 parts")
+    if any(p.dtype != torch.float32 for p in parts) or dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("concat_cast: float32 parts, bf16 or float32 output")
+    if any(p.shape[:-1] != parts[0].shape[:-1] or p.shape[-1] % 4 for p in parts):
+        raise ValueError("concat_cast: one leading shape, last extents multiples of 4")
+    return _ConcatCast.apply(dtype, *parts)
+
+
+__all__ = ["heads_to_tokens", "transpose_last2", "concat_cast"]

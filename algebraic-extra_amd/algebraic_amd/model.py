@@ -10,8 +10,10 @@ product (and SwiGLU's), the attention prologue (QK-norm, rotation and the
 layout change in one pass, for 64-wide heads) and, with
 ``head_impl="fused"``, the LM head + loss. The projections are plain bf16
 GEMMs (hipBLASLt through torch), with q/k/v and gate/up each fused into one
-GEMM; the rotation tables, the dense head and, for other head widths, the
-rotate-half product are torch ops.
+GEMM whose joined bf16 weights are cast once per step (libalgx concat_cast),
+and the attention output's head-to-token layout change is a libalgx pass; the
+rotation tables, the dense head and, for other head widths, the rotate-half
+product are torch ops.
 
 ``remat=True`` recomputes each block in the backward
 (``torch.utils.checkpoint``), as ``jax.checkpoint`` does (model.py:205-206).
@@ -30,7 +32,7 @@ from .kernels.flash import flash_attention
 from .kernels.fused_head import fused_head
 from .kernels.prologue import attention_prologue
 from .kernels.qk_norm import qk_rms_norm
-from .layout import heads_to_tokens
+from .layout import concat_cast, heads_to_tokens
 
 F32 = torch.float32
 _DTYPES = {"bfloat16": torch.bfloat16, "float32": torch.float32}
@@ -320,6 +322,15 @@ def _block(cfg: LMConfig, cos, sin, x, r, lp):
     return x, y @ lp["w_d_c"]
 
 
+def _joined(parts, dt):
+    """torch.cat(parts, -1).to(dt) of float32 stacked weights: one libalgx pass
+    each way on the device when every width is a multiple of 4."""
+    if (parts[0].is_cuda and all(p.dtype == F32 for p in parts)
+            and all(p.shape[-1] % 4 == 0 for p in parts)):
+        return concat_cast(parts, dt)
+    return torch.cat(parts, dim=-1).to(dt)
+
+
 def forward_hidden(params, tokens: torch.Tensor, cfg: LMConfig, tables) -> torch.Tensor:
     """Final normalised hidden states (B, T, d) in the compute dtype (model.py:194-208)."""
     cos, sin = tables
@@ -336,10 +347,9 @@ def forward_hidden(params, tokens: torch.Tensor, cfg: LMConfig, tables) -> torch
     per_layer = {name: t.unbind(0) for name, t in layers.items()}
     per_layer["w_o_c"] = layers["w_o"].to(dt).unbind(0)
     per_layer["w_d_c"] = layers["w_d"].to(dt).unbind(0)
-    per_layer["w_gu"] = torch.cat([layers["w_g"], layers["w_u"]], dim=2).to(dt).unbind(0)
+    per_layer["w_gu"] = _joined([layers["w_g"], layers["w_u"]], dt).unbind(0)
     if cfg.head_dim == 64:
-        per_layer["w_qkv"] = torch.cat([layers["w_q"], layers["w_k"], layers["w_v"]],
-                                       dim=2).to(dt).unbind(0)
+        per_layer["w_qkv"] = _joined([layers["w_q"], layers["w_k"], layers["w_v"]], dt).unbind(0)
     r = None
     for i in range(cfg.n_layers):
         lp = {name: ts[i] for name, ts in per_layer.items()}

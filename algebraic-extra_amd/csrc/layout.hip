@@ -9,8 +9,13 @@
 //   M and N multiples of the 16-byte vector (8 bf16 or 4 float32) every lane
 //   transposes one square block in registers (no LDS); other shapes go
 //   through a 64 x 64 LDS tile.
+// * concat_cast / split_cast: float32 [rows][C_i] parts (up to 4) written as
+//   one [rows][sum C_i] bf16 or float32 matrix, and the inverse for the
+//   gradient: the per-step casts and concatenations of the layer-stacked
+//   weights for the fused [w_q | w_k | w_v] and [w_g | w_u] GEMMs
+//   (model.py:167-169, :184-189 cast each weight to the compute dtype).
 //
-// Both are HBM-bound byte moves: every source byte is read once and every
+// All are HBM-bound byte moves: every source byte is read once and every
 // destination byte written once, in 128-byte (or longer) runs per wave.
 #include "common.h"
 
@@ -105,6 +110,97 @@ __global__ __launch_bounds__(kThreads) void transpose_block_kernel(const i32x4* 
   for (int c = 0; c < V; ++c) dst[base + (int64_t)(n0 + c) * mv + m0 / V] = out[c];
 }
 
+constexpr int kMaxParts = 4;
+
+struct Parts {
+  void* p[kMaxParts];   // float32 parts
+  int64_t c[kMaxParts];  // columns of each part (multiples of 4)
+  int64_t off[kMaxParts + 1];  // column offset of each part in the joined matrix
+  int n;
+};
+
+// One 4-column group of the joined matrix per thread: the group lies inside
+// one part (its columns are multiples of 4). TO_JOINED: parts -> joined
+// (float32 read, T written); otherwise joined -> parts (T read, float32 written).
+template <typename T, bool TO_JOINED>
+__global__ __launch_bounds__(kThreads) void concat_cast_kernel(Parts parts, T* __restrict__ joined,
+                                                               int64_t rows) {
+  const int64_t w = parts.off[parts.n];
+  const int64_t groups = w / 4;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= rows * groups) return;
+  const int64_t r = i / groups, col = (i % groups) * 4;
+  int q = 0;
+#pragma unroll
+  for (int t = 1; t < kMaxParts; ++t) q += (t < parts.n && col >= parts.off[t]) ? 1 : 0;
+  float* part = (float*)parts.p[q] + r * parts.c[q] + (col - parts.off[q]);
+  T* jp = joined + r * w + col;
+  if (TO_JOINED) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(part);
+    if (sizeof(T) == 2) {
+      bf16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (bf16)v[e];
+      *reinterpret_cast<bf16x4*>(jp) = o;
+    } else {
+      *reinterpret_cast<f32x4*>(jp) = v;
+    }
+  } else {
+    f32x4 v;
+    if (sizeof(T) == 2) {
+      const bf16x4 b = *reinterpret_cast<const bf16x4*>(jp);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (float)b[e];
+    } else {
+      v = *reinterpret_cast<const f32x4*>(jp);
+    }
+    *reinterpret_cast<f32x4*>(part) = v;
+  }
+}
+
+int32_t concat_cast_any(void* const* parts, const int64_t* cols, int32_t nparts, void* joined,
+                        int64_t rows, int32_t dtype, bool to_joined, void* stream) {
+  const char* what = to_joined ? "concat_cast" : "split_cast";
+  if (nparts < 1 || nparts > kMaxParts) return fail(std::string(what) + ": 1 to 4 parts");
+  if (rows < 0) return fail(std::string(what) + ": negative row count");
+  if (dtype != ALGX_BF16 && dtype != ALGX_F32) return fail(std::string(what) + ": dtype must be bf16 or f32");
+  Parts ps{};
+  ps.n = nparts;
+  ps.off[0] = 0;
+  for (int i = 0; i < nparts; ++i) {
+    if (cols[i] <= 0 || cols[i] % 4) return fail(std::string(what) + ": part widths must be positive multiples of 4");
+    ps.p[i] = parts[i];
+    ps.c[i] = cols[i];
+    ps.off[i + 1] = ps.off[i] + cols[i];
+  }
+  const int64_t total = rows * (ps.off[nparts] / 4);
+  if (total == 0) return 0;
+  if (joined == nullptr || ((uintptr_t)joined & (dtype == ALGX_BF16 ? 7 : 15)))
+    return fail(std::string(what) + ": joined matrix null or misaligned");
+  for (int i = 0; i < nparts; ++i)
+    if (parts[i] == nullptr || !((((uintptr_t)parts[i]) & 15) == 0))
+      return fail(std::string(what) + ": parts must be 16-byte aligned float32");
+  const int64_t blocks = (total + kThreads - 1) / kThreads;
+  if (blocks >= ((int64_t)1 << 31)) return fail(std::string(what) + ": too many elements");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ALGX_BF16) {
+    if (to_joined)
+      hipLaunchKernelGGL((concat_cast_kernel<bf16, true>), dim3((uint32_t)blocks), dim3(kThreads),
+                         0, s, ps, (bf16*)joined, rows);
+    else
+      hipLaunchKernelGGL((concat_cast_kernel<bf16, false>), dim3((uint32_t)blocks), dim3(kThreads),
+                         0, s, ps, (bf16*)joined, rows);
+  } else {
+    if (to_joined)
+      hipLaunchKernelGGL((concat_cast_kernel<float, true>), dim3((uint32_t)blocks),
+                         dim3(kThreads), 0, s, ps, (float*)joined, rows);
+    else
+      hipLaunchKernelGGL((concat_cast_kernel<float, false>), dim3((uint32_t)blocks),
+                         dim3(kThreads), 0, s, ps, (float*)joined, rows);
+  }
+  return check_launch(what);
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 bool overlaps(const void* a, const void* b, int64_t bytes) {
@@ -169,4 +265,14 @@ extern "C" int32_t algx_transpose(const void* src, void* dst, int64_t K, int64_t
     hipLaunchKernelGGL(transpose_kernel<uint32_t>, grid, dim3(kThreads), 0, s,
                        (const uint32_t*)src, (uint32_t*)dst, (int)M, (int)N, (int)tiles_n);
   return check_launch("transpose");
+}
+
+extern "C" int32_t algx_concat_cast(void* const* parts, const int64_t* cols, int32_t nparts,
+                                   void* joined, int64_t rows, int32_t dtype, void* stream) {
+  return concat_cast_any(parts, cols, nparts, joined, rows, dtype, true, stream);
+}
+
+extern "C" int32_t algx_split_cast(const void* joined, void* const* parts, const int64_t* cols,
+                                  int32_t nparts, int64_t rows, int32_t dtype, void* stream) {
+  return concat_cast_any(parts, cols, nparts, (void*)joined, rows, dtype, false, stream);
 }

@@ -253,6 +253,17 @@ int32_t algx_swap_axes(const void* src, void* dst, int64_t B, int64_t P, int64_t
                        int64_t row_bytes, void* stream);
 int32_t algx_transpose(const void* src, void* dst, int64_t K, int64_t M, int64_t N,
                        int32_t elem_bytes, void* stream);
+/* algx_concat_cast: joined [rows][sum cols] (bf16 or float32, dtype) from
+ * nparts (1 to 4) float32 parts [rows][cols[i]], cols[i] positive multiples of
+ * 4, parts 16-byte and joined 8- (bf16) or 16-byte (f32) aligned, none
+ * overlapping. algx_split_cast: the inverse (the gradient of the parts). The
+ * model's per-step compute-dtype copies of the stacked weights
+ * (src/algebraic/model.py:167-169, :184-189 cast each weight per block) joined
+ * for the fused [w_q | w_k | w_v] and [w_g | w_u] GEMMs. */
+int32_t algx_concat_cast(void* const* parts, const int64_t* cols, int32_t nparts, void* joined,
+                         int64_t rows, int32_t dtype, void* stream);
+int32_t algx_split_cast(const void* joined, void* const* parts, const int64_t* cols,
+                        int32_t nparts, int64_t rows, int32_t dtype, void* stream);
 
 /* ------------------------------------------------------------- Muon steps
  * The elementwise parts of Muon's update (src/algebraic/optimizers.py:200-204)

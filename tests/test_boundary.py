@@ -170,3 +170,19 @@ def test_layout_validation_without_a_gpu():
         heads_to_tokens(_t((1, 2, 3, 4)))
     with pytest.raises(ValueError, match="2 or 4 bytes"):
         transpose_last2(_t((3, 4), torch.float64))
+
+
+def test_concat_cast_validation_without_a_gpu():
+    from algebraic_amd.layout import concat_cast
+    with pytest.raises(ValueError, match="1 to 4 parts"):
+        concat_cast([_t((2, 4), torch.float32)] * 5, torch.bfloat16)
+    with pytest.raises(ValueError, match="float32 parts"):
+        concat_cast([_t((2, 4))], torch.bfloat16)
+    with pytest.raises(ValueError, match="multiples of 4"):
+        concat_cast([_t((2, 6), torch.float32)], torch.bfloat16)
+    lib = _lib.load()
+    cols = (ctypes.c_int64 * 1)(6)
+    parts = (ctypes.c_void_p * 1)(16)
+    assert lib.algx_concat_cast(ctypes.cast(parts, ctypes.c_void_p), ctypes.cast(cols, ctypes.c_void_p),
+                                1, ctypes.c_void_p(64), 2, 0, None) != 0
+    assert b"multiples of 4" in lib.algx_last_error()

@@ -75,3 +75,25 @@ def test_transpose_matches_torch(shape, dtype):
 def test_transpose_empty():
     x = torch.empty((3, 0, 5), device=DEV, dtype=torch.bfloat16)
     assert transpose_last2(x).shape == (3, 5, 0)
+
+
+@pytest.mark.parametrize("widths,lead,dtype", [
+    ((1024, 1024, 1024), (24, 1024), torch.bfloat16),
+    ((2688, 2688), (24, 1024), torch.bfloat16),
+    ((8, 12, 4), (3, 5), torch.bfloat16),
+    ((16, 20), (2, 7), torch.float32),
+    ((4,), (1, 1), torch.bfloat16),
+])
+def test_concat_cast_matches_torch(widths, lead, dtype):
+    """concat_cast == torch.cat(parts, -1).to(dtype) bit for bit (float32 ->
+    bf16 rounds to nearest even in both), and its gradient is the split of
+    the incoming gradient cast to float32."""
+    from algebraic_amd.layout import concat_cast
+    parts = [_rand(lead + (w,), torch.float32, 30 + i).requires_grad_(True)
+             for i, w in enumerate(widths)]
+    out = concat_cast(parts, dtype)
+    assert out.dtype == dtype and torch.equal(out, torch.cat([p.detach() for p in parts], -1).to(dtype))
+    g = _rand(out.shape, dtype, 40)
+    grads = torch.autograd.grad(out, parts, g)
+    for got, want in zip(grads, g.float().split(list(widths), dim=-1)):
+        assert got.dtype == torch.float32 and torch.equal(got, want)
