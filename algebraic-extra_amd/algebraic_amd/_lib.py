@@ -73,6 +73,7 @@ SIGNATURES = {
     "algx_split_cast": (_i32, [_p, _p, _p, _i32, _i64, _i32, _p]),
     "algx_muon_momentum": (_i32, [_p, _p, _p, _i64, _f32, _p]),
     "algx_muon_apply": (_i32, [_p, _p, _i64, _i32, _f32, _f32, _p]),
+    "algx_adamw_step": (_i32, [_p, _p, _p, _p, _i64, _f32, _f32, _f32, _f32, _f32, _f32, _f32, _p]),
     "algx_ns_normalize_workspace_bytes": (_i64, [_i64, _i64]),
     "algx_ns_normalize": (_i32, [_p, _p, _i64, _i64, _i32, _f32, _p, _p]),
     "algx_qk_prologue_fwd": (_i32, [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,

@@ -69,6 +69,20 @@ def _muon_apply(p: torch.Tensor, o: torch.Tensor, decay_fac: float, step: float)
     p.add_(o.to(F32), alpha=-step)
 
 
+def _fused_ok(*ts) -> bool:
+    return all(t.is_cuda and t.dtype == F32 and t.is_contiguous() and t.data_ptr() % 16 == 0
+               for t in ts)
+
+
+def _adamw_step(p, g, m, v, b1, b2, c1, c2, eps, decay_fac, lr) -> None:
+    """The Adam leaf update of optimizers.py:222-226 in place, one libalgx pass
+    (m, v and p read and written once, g read once)."""
+    g = _aligned(g.to(F32))
+    _lib.call("algx_adamw_step", _lib.ptr(p), _lib.ptr(g), _lib.ptr(m), _lib.ptr(v), p.numel(),
+              float(b1), float(b2), float(c1), float(c2), float(eps), float(decay_fac),
+              float(lr), _lib.stream())
+
+
 _NS_ABC = (3.4445, -4.7750, 2.0315)
 
 
@@ -278,6 +292,10 @@ def get_optimizer(name: str, lr: float, weight_decay: float = 0.1, total_steps: 
             if uses_muon and is_muon_param(path, p):
                 # m <- mu m + (1 - mu) g and the Nesterov look-ahead, orthogonalised below
                 muon_jobs.append((p, decay, _muon_momentum(g, m, muon_momentum)))
+                continue
+            decay_fac = 1.0 - adam_lr * weight_decay if decay else 1.0
+            if opt_name == "muon_adamw" and _fused_ok(p, m, v):
+                _adamw_step(p, g, m, v, b1, b2, c1, c2, adam_eps, decay_fac, adam_lr)
                 continue
             m.mul_(b1).add_(g, alpha=1.0 - b1)
             v.mul_(b2).addcmul_(g, g, value=1.0 - b2)

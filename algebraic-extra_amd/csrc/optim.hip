@@ -8,6 +8,9 @@
 // * apply: p <- p * decay - step * o for the orthogonalised update o (bf16 or
 //   float32), step = lr times the aspect factor of newton_schulz_5. Reads p,
 //   o; writes p.
+// * adamw: the Adam-family leaves' step (optimizers.py:222-226): m, v, the
+//   bias-corrected update and the decayed parameter in one pass (reads p, g,
+//   m, v; writes p, m, v: 28 bytes per element).
 // * ns_normalize: X / sqrt(sum(X^2) + eps) per matrix, cast to the
 //   Newton-Schulz input type (optimizers.py:44-45): per-block sums of squares
 //   of each matrix, then one pass that reduces its matrix's partials (fixed
@@ -73,6 +76,44 @@ __global__ __launch_bounds__(kThreads) void muon_apply_kernel(float* __restrict_
     *reinterpret_cast<f32x4*>(p + i) = pv;
   } else {
     for (int64_t j = i; j < n; ++j) p[j] = p[j] * decay - step * to_f(o[j]);
+  }
+}
+
+__device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v, float b1,
+                                           float b2, float c1, float c2, float eps, float decay,
+                                           float lr) {
+  m = b1 * m + (1.0f - b1) * g;
+  v = b2 * v + (1.0f - b2) * (g * g);
+  const float u = (m / c1) / (__builtin_sqrtf(v / c2) + eps);
+  p = p * decay - lr * u;
+}
+
+__global__ __launch_bounds__(kThreads) void adamw_kernel(float* __restrict__ p,
+                                                         const float* __restrict__ g,
+                                                         float* __restrict__ m,
+                                                         float* __restrict__ v, int64_t n, float b1,
+                                                         float b2, float c1, float c2, float eps,
+                                                         float decay, float lr) {
+  const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
+  if (i >= n) return;
+  if (i + 4 <= n) {
+    f32x4 pv = *reinterpret_cast<const f32x4*>(p + i);
+    const f32x4 gv = *reinterpret_cast<const f32x4*>(g + i);
+    f32x4 mv = *reinterpret_cast<const f32x4*>(m + i);
+    f32x4 vv = *reinterpret_cast<const f32x4*>(v + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float pe = pv[e], me = mv[e], ve = vv[e];
+      adamw_elem(pe, gv[e], me, ve, b1, b2, c1, c2, eps, decay, lr);
+      pv[e] = pe;
+      mv[e] = me;
+      vv[e] = ve;
+    }
+    *reinterpret_cast<f32x4*>(p + i) = pv;
+    *reinterpret_cast<f32x4*>(m + i) = mv;
+    *reinterpret_cast<f32x4*>(v + i) = vv;
+  } else {
+    for (int64_t j = i; j < n; ++j) adamw_elem(p[j], g[j], m[j], v[j], b1, b2, c1, c2, eps, decay, lr);
   }
 }
 
@@ -249,4 +290,18 @@ extern "C" int32_t algx_ns_normalize(const float* x, void* out, int64_t K, int64
                          (float*)out, MN, span, eps);
   }
   return check_launch("ns_scale");
+}
+
+extern "C" int32_t algx_adamw_step(float* p, const float* g, float* m, float* v, int64_t n,
+                                  float b1, float b2, float c1, float c2, float eps, float decay,
+                                  float lr, void* stream) {
+  if (n < 0) return fail("adamw_step: negative size");
+  if (n == 0) return 0;
+  if (p == nullptr || g == nullptr || m == nullptr || v == nullptr) return fail("adamw_step: null pointer");
+  if (!aligned16(p) || !aligned16(g) || !aligned16(m) || !aligned16(v))
+    return fail("adamw_step: pointers must be 16-byte aligned");
+  if (blocks_of(n) >= ((int64_t)1 << 31)) return fail("adamw_step: too many elements");
+  hipLaunchKernelGGL(adamw_kernel, dim3((uint32_t)blocks_of(n)), dim3(kThreads), 0,
+                     (hipStream_t)stream, p, g, m, v, n, b1, b2, c1, c2, eps, decay, lr);
+  return check_launch("adamw_step");
 }

@@ -278,6 +278,13 @@ int32_t algx_muon_momentum(const float* g, float* m, float* look, int64_t n, flo
                            void* stream);
 int32_t algx_muon_apply(float* p, const void* o, int64_t n, int32_t o_dtype, float decay,
                         float step, void* stream);
+/* algx_adamw_step: the Adam-family leaf update (optimizers.py:222-226) over n
+ * float32 elements in place: m = b1 m + (1 - b1) g, v = b2 v + (1 - b2) g^2,
+ * p = p * decay - lr * (m / c1) / (sqrt(v / c2) + eps), with c1, c2 the bias
+ * corrections 1 - b^t and decay = 1 - lr * wd for decayed leaves (else 1). */
+int32_t algx_adamw_step(float* p, const float* g, float* m, float* v, int64_t n, float b1,
+                        float b2, float c1, float c2, float eps, float decay, float lr,
+                        void* stream);
 /* algx_ns_normalize: out[k] = cast(x[k] / sqrt(sum(x[k]^2) + eps)) for K float32
  * matrices of MN elements (newton_schulz_5's pre-normalisation,
  * src/algebraic/optimizers.py:44-45), out in bf16 or float32 (out_dtype),

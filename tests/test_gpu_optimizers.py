@@ -102,3 +102,24 @@ def test_ns_normalize_kernel(shape, out_dtype):
     got = out.double().cpu()
     tol = 2.0 ** -8 if out_dtype == torch.bfloat16 else 4e-6
     assert float(((got - want).abs() / want.abs().clamp_min(1e-30)).max()) <= tol
+
+
+@pytest.mark.parametrize("n", [1, 5, 4096, 51513])
+def test_adamw_step_kernel(n):
+    """algx_adamw_step against optimizers.py:222-226 in float64 from the same
+    float32 state (a few float32 ulp)."""
+    rng = np.random.default_rng(n + 1)
+    p64, g64, m64 = (rng.standard_normal(n) for _ in range(3))
+    v64 = rng.random(n) * 0.1
+    ts = [torch.tensor(a, dtype=torch.float32, device=DEV) for a in (p64, g64, m64, v64)]
+    b1, b2, eps, lr, decay = 0.9, 0.95, 1e-8, 2e-3, 1.0 - 2e-3 * 0.1
+    t = 3.0
+    c1, c2 = 1.0 - b1 ** t, 1.0 - b2 ** t
+    O._adamw_step(ts[0], ts[1], ts[2], ts[3], b1, b2, c1, c2, eps, decay, lr)
+    p, g, m, v = (a.astype(np.float32).astype(np.float64) for a in (p64, g64, m64, v64))
+    m = b1 * m + (1 - b1) * g
+    v = b2 * v + (1 - b2) * g * g
+    p = p * decay - lr * (m / c1) / (np.sqrt(v / c2) + eps)
+    np.testing.assert_allclose(ts[2].double().cpu().numpy(), m, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(ts[3].double().cpu().numpy(), v, rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(ts[0].double().cpu().numpy(), p, rtol=1e-6, atol=1e-6)
