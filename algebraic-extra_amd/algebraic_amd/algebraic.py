@@ -10,7 +10,7 @@ recomputing ``u`` and ``r`` from the saved input instead of storing them.
 
 Inputs are bfloat16 or float32 CUDA (ROCm) tensors; ``rms_norm`` normalises
 the last axis (a multiple of 8 values for bfloat16, of 4 for float32, at most
-1024) and takes its gain as float32 (any other gain dtype is converted, and
+2048) and takes its gain as float32 (any other gain dtype is converted, and
 its gradient returned in that dtype).
 """
 
@@ -63,9 +63,9 @@ def rms_norm(x: torch.Tensor, gain: Optional[torch.Tensor], eps: float = 1e-5) -
         raise ValueError("rms_norm kernel needs float32 or bfloat16 input")
     D = x.shape[-1] if x.ndim else 0
     width = 8 if x.dtype == torch.bfloat16 else 4
-    if D <= 0 or D % width or D > 1024:
+    if D <= 0 or D % width or D > 2048:
         raise NotImplementedError(f"rms_norm kernel needs a last axis that is a multiple of {width}"
-                                  f" and at most 1024, got {D}")
+                                  f" and at most 2048, got {D}")
     if gain is not None and tuple(gain.shape) != (D,):
         raise ValueError(f"gain must have shape ({D},)")
     if not eps > 0:
@@ -120,9 +120,9 @@ def add_rms_norm(x: torch.Tensor, r: torch.Tensor, gain: Optional[torch.Tensor],
         raise ValueError("rms_norm kernel needs float32 or bfloat16 input")
     D = x.shape[-1] if x.ndim else 0
     width = 8 if x.dtype == torch.bfloat16 else 4
-    if D <= 0 or D % width or D > 1024:
+    if D <= 0 or D % width or D > 2048:
         raise NotImplementedError(f"rms_norm kernel needs a last axis that is a multiple of {width}"
-                                  f" and at most 1024, got {D}")
+                                  f" and at most 2048, got {D}")
     if gain is not None and tuple(gain.shape) != (D,):
         raise ValueError(f"gain must have shape ({D},)")
     if not eps > 0:

@@ -317,7 +317,7 @@ __device__ __forceinline__ void fwd_body(
       for (int i = 0; i < 4; ++i) val[i] = oacc[dt][4 * j + i] * inv;
       bf16x4 ob = {(bf16)val[0], (bf16)val[1], (bf16)val[2], (bf16)val[3]};
       *reinterpret_cast<bf16x4*>(o + orow + d) = ob;
-      if (MODE == MODE_SHIFT && var.precise && o_precise != nullptr)
+      if (var.precise && o_precise != nullptr)
         *reinterpret_cast<f32x4*>(o_precise + orow + d) = val;
     }
   if (g == 0) stat[(int64_t)bh * T_ + qrow] = final_stat(var, m_row, l_tot);

@@ -21,7 +21,7 @@ namespace {
 constexpr int kFwdThreads = 256;
 constexpr int kBwdThreads = 1024;
 constexpr int kBwdWaves = kBwdThreads / 64;
-constexpr int kMaxD = 1024;
+constexpr int kMaxD = 2048;
 constexpr int kMaxBwdBlocks = 512;
 constexpr int kEltThreads = 256;
 
@@ -119,7 +119,9 @@ __global__ __launch_bounds__(kBwdThreads) void rmsnorm_bwd_kernel(
     const T* __restrict__ dres) {
   typedef typename Vec<T>::type VT;
   constexpr int EPL = Vec<T>::n;
-  __shared__ float red[kBwdWaves][kMaxD];
+  // One row of column sums per wave, as wide as the widest row this
+  // instantiation takes (64 KB at CPL * EPL = 16).
+  __shared__ float red[kBwdWaves][64 * CPL * EPL];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int nch = D / EPL;
   float g[CPL][EPL], dg[CPL][EPL];
@@ -349,7 +351,7 @@ int32_t check_norm(const void* x, int64_t rows, int32_t D, int32_t dtype, float 
   if (dtype != ALGX_BF16 && dtype != ALGX_F32) return fail("rms_norm: dtype must be bf16 or f32");
   if (rows < 0) return fail("rms_norm: negative row count");
   if (D <= 0 || D > kMaxD || D % epl_of(dtype))
-    return fail("rms_norm: D must be a multiple of 8 (bf16) or 4 (f32), at most 1024");
+    return fail("rms_norm: D must be a multiple of 8 (bf16) or 4 (f32), at most 2048");
   if (!(eps > 0.0f)) return fail("rms_norm: eps must be positive");
   if (rows > 0 && x == nullptr) return fail("rms_norm: null input");
   return 0;
@@ -405,13 +407,21 @@ int32_t norm_fwd_impl(const void* x, const void* r, const float* gain, void* xsu
   // Chunks per lane: ceil(D / (16-byte elements) / 64).
   const int cpl = (D / epl_of(dtype) + 63) / 64;
   if (dtype == ALGX_BF16) {
-    if (cpl == 1) launch_norm_fwd<bf16, 1>(x, gain, y, rows, D, eps, r, xsum, s);
-    else launch_norm_fwd<bf16, 2>(x, gain, y, rows, D, eps, r, xsum, s);
+    switch (cpl) {
+      case 1: launch_norm_fwd<bf16, 1>(x, gain, y, rows, D, eps, r, xsum, s); break;
+      case 2: launch_norm_fwd<bf16, 2>(x, gain, y, rows, D, eps, r, xsum, s); break;
+      case 3: launch_norm_fwd<bf16, 3>(x, gain, y, rows, D, eps, r, xsum, s); break;
+      default: launch_norm_fwd<bf16, 4>(x, gain, y, rows, D, eps, r, xsum, s); break;
+    }
   } else {
-    if (cpl == 1) launch_norm_fwd<float, 1>(x, gain, y, rows, D, eps, r, xsum, s);
-    else if (cpl == 2) launch_norm_fwd<float, 2>(x, gain, y, rows, D, eps, r, xsum, s);
-    else if (cpl == 3) launch_norm_fwd<float, 3>(x, gain, y, rows, D, eps, r, xsum, s);
-    else launch_norm_fwd<float, 4>(x, gain, y, rows, D, eps, r, xsum, s);
+    switch (cpl) {
+      case 1: launch_norm_fwd<float, 1>(x, gain, y, rows, D, eps, r, xsum, s); break;
+      case 2: launch_norm_fwd<float, 2>(x, gain, y, rows, D, eps, r, xsum, s); break;
+      case 3: launch_norm_fwd<float, 3>(x, gain, y, rows, D, eps, r, xsum, s); break;
+      case 4: launch_norm_fwd<float, 4>(x, gain, y, rows, D, eps, r, xsum, s); break;
+      case 5: case 6: launch_norm_fwd<float, 6>(x, gain, y, rows, D, eps, r, xsum, s); break;
+      default: launch_norm_fwd<float, 8>(x, gain, y, rows, D, eps, r, xsum, s); break;
+    }
   }
   return check_launch("rms_norm_fwd");
 }
@@ -431,13 +441,21 @@ int32_t norm_bwd_impl(const void* x, const float* gain, const void* dy, const vo
   float* partial = gain != nullptr ? (float*)workspace : nullptr;
   const int cpl = (D / epl_of(dtype) + 63) / 64;
   if (dtype == ALGX_BF16) {
-    if (cpl == 1) launch_norm_bwd<bf16, 1>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
-    else launch_norm_bwd<bf16, 2>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
+    switch (cpl) {
+      case 1: launch_norm_bwd<bf16, 1>(x, gain, dy, dx, partial, rows, D, eps, dres, s); break;
+      case 2: launch_norm_bwd<bf16, 2>(x, gain, dy, dx, partial, rows, D, eps, dres, s); break;
+      case 3: launch_norm_bwd<bf16, 3>(x, gain, dy, dx, partial, rows, D, eps, dres, s); break;
+      default: launch_norm_bwd<bf16, 4>(x, gain, dy, dx, partial, rows, D, eps, dres, s); break;
+    }
   } else {
-    if (cpl == 1) launch_norm_bwd<float, 1>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
-    else if (cpl == 2) launch_norm_bwd<float, 2>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
-    else if (cpl == 3) launch_norm_bwd<float, 3>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
-    else launch_norm_bwd<float, 4>(x, gain, dy, dx, partial, rows, D, eps, dres, s);
+    switch (cpl) {
+      case 1: launch_norm_bwd<float, 1>(x, gain, dy, dx, partial, rows, D, eps, dres, s); break;
+      case 2: launch_norm_bwd<float, 2>(x, gain, dy, dx, partial, rows, D, eps, dres, s); break;
+      case 3: launch_norm_bwd<float, 3>(x, gain, dy, dx, partial, rows, D, eps, dres, s); break;
+      case 4: launch_norm_bwd<float, 4>(x, gain, dy, dx, partial, rows, D, eps, dres, s); break;
+      case 5: case 6: launch_norm_bwd<float, 6>(x, gain, dy, dx, partial, rows, D, eps, dres, s); break;
+      default: launch_norm_bwd<float, 8>(x, gain, dy, dx, partial, rows, D, eps, dres, s); break;
+    }
   }
   if (int32_t rc = check_launch("rms_norm_bwd")) return rc;
   if (gain == nullptr) return 0;

@@ -16,7 +16,7 @@
 #include <cstdlib>
 #include <type_traits>
 
-#include "common.h"
+#include "head_f32.h"
 
 namespace algx {
 
@@ -517,8 +517,8 @@ int chunk_tokens(int N, int V) {
 int32_t check_head(const void* h, const void* E, const int32_t* targets, int N, int d, int V,
                    int kind, int n, int dtype) {
   if (N < 0 || d <= 0 || V <= 0) return fail("head: invalid sizes");
-  if (dtype != ALGX_BF16) return fail("head: the MFMA head takes bfloat16 hidden states");
-  if (d % 8) return fail("head: hidden width must be a multiple of 8");
+  if (dtype != ALGX_BF16 && dtype != ALGX_F32) return fail("head: dtype must be bf16 or f32");
+  if (dtype == ALGX_BF16 && d % 8) return fail("head: hidden width must be a multiple of 8");
   if (kind != ALGX_HEAD_CE && kind != ALGX_HEAD_ALG_CE) return fail("head: unknown kind");
   if (kind == ALGX_HEAD_ALG_CE && (n < 1 || (n & (n - 1)))) return fail("head: n must be a power of two");
   if (N > 0 && (h == nullptr || E == nullptr || targets == nullptr)) return fail("head: null input");
@@ -562,7 +562,8 @@ using namespace algx;
 
 extern "C" int64_t algx_head_fwd_workspace_bytes(int32_t N, int32_t d, int32_t V, int32_t dtype) {
   (void)d;
-  (void)dtype;
+  if (N <= 0 || V <= 0) return 0;
+  if (dtype == ALGX_F32) return head_f32_fwd_workspace(N, V);
   return (int64_t)nchunks_of(V) * N * 2 * sizeof(float);
 }
 
@@ -581,6 +582,9 @@ extern "C" int32_t algx_head_fwd(const void* h, const void* E, const int32_t* ta
   // The target logit starts at 0 as in fused_head.py:80 (a target outside
   // the vocabulary tiles is never met).
   if (int32_t rc = fill_f32(zt, N, 0.0f, s)) return rc;
+  if (dtype == ALGX_F32)
+    return head_f32_fwd((const float*)h, (const float*)E, targets, stat, zt, partial, N, d, V,
+                        kind, log2n, inv_c, clamp, s);
   {
     const Probe probe = probe_for(ALGX_PROBE_HEAD_FWD);
     launch_k(probe, pick_head_fwd(kind, log2n),
@@ -598,8 +602,8 @@ extern "C" int32_t algx_head_fwd(const void* h, const void* E, const int32_t* ta
 
 extern "C" int64_t algx_head_bwd_workspace_bytes(int32_t N, int32_t d, int32_t V, int32_t dtype) {
   (void)d;
-  (void)dtype;
-  if (N <= 0) return 0;
+  if (N <= 0 || V <= 0) return 0;
+  if (dtype == ALGX_F32) return head_f32_bwd_workspace(N, V);
   return (int64_t)chunk_tokens(N, V) * vpad_of(V) * 2;
 }
 
@@ -615,6 +619,9 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
   if (stat == nullptr || scale == nullptr || dh == nullptr || workspace == nullptr)
     return fail("head_bwd: null pointer");
   const int log2n = kind == ALGX_HEAD_ALG_CE ? ilog2(n) : 0;
+  if (dtype == ALGX_F32)
+    return head_f32_bwd((const float*)h, (const float*)E, targets, stat, scale, (float*)dh, dE,
+                        (float*)workspace, N, d, V, kind, log2n, inv_c, clamp, s);
   const int64_t ldz = vpad_of(V);
   const int csize = chunk_tokens(N, V);
   bf16* dz = (bf16*)workspace;

@@ -372,6 +372,54 @@ def cpu_baseline(B, H, T, D, heads=None, runs=6):
                       f"fwd + autograd bwd in torch-CPU float32"}
 
 
+def calibrate_copy(dev):
+    """One plain 256 MiB device copy: the scale reference for the FETCH_SIZE /
+    WRITE_SIZE counters of a rocprofv3 --pmc run (it must read 262144 KiB and
+    write 262144 KiB)."""
+    import torch
+    src = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+
+
+def run_once(which, dev, steps=3):
+    """`steps` untimed steps of one benchmark workload (for counter passes)."""
+    import torch
+    if which in ("attn", "attn16"):
+        from algebraic_amd.kernels import flash_attention
+        H = 12 if which == "attn" else 16
+        q, k, v, do = make_attention_inputs(8, H, 2048, 64, 1, dev)
+        for _ in range(steps):
+            o = flash_attention(q, k, v, kind="asinh", n=16, c=8.0, range_guard=True)
+            torch.autograd.grad(o, (q, k, v), do)
+    elif which == "head":
+        from algebraic_amd.kernels import fused_head
+        N, d, V = 16384, 768, 50304
+        gen = torch.Generator(device=dev).manual_seed(2)
+        h = torch.randn((N, d), device=dev, generator=gen).bfloat16().requires_grad_(True)
+        E = (torch.randn((V, d), device=dev, generator=gen) * 0.02).bfloat16().requires_grad_(True)
+        t = torch.randint(0, V, (N,), device=dev, generator=gen, dtype=torch.int64)
+        for _ in range(steps):
+            obj, _ = fused_head(h, E, t, kind="alg_ce", n=8, c=2.0)
+            torch.autograd.grad(obj, (h, E))
+    else:
+        from algebraic_amd.kernels import qk_rms_norm
+        gen = torch.Generator(device=dev).manual_seed(3)
+        shape = (8, 2048, 16, 64)
+        xs = [torch.randn(shape, device=dev, generator=gen).bfloat16().requires_grad_(True)
+              for _ in range(2)]
+        gains = [(1 + 0.01 * torch.randn(64, device=dev, generator=gen)).requires_grad_(True)
+                 for _ in range(2)]
+        dys = [torch.randn(shape, device=dev, generator=gen).bfloat16() for _ in range(2)]
+        for _ in range(steps):
+            for x, g, dy in zip(xs, gains, dys):
+                torch.autograd.grad(qk_rms_norm(x, g), (x, g), dy)
+    torch.cuda.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -385,6 +433,10 @@ def main():
                     help="print only the 350M model lines (algebraic and standard)")
     ap.add_argument("--elementwise-only", action="store_true",
                     help="print only the rms_norm / alu_glu line")
+    ap.add_argument("--once", choices=("attn", "attn16", "head", "qknorm"),
+                    help="run three untimed steps of one workload and exit, printing nothing "
+                         "else: the command for rocprofv3 counter passes (configs[1] attention, "
+                         "configs[3] attention, configs[2] head, configs[3] QK-norm)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 256 MiB device copy (scale reference for the "
                          "FETCH_SIZE/WRITE_SIZE counters of a rocprofv3 --pmc run)")
@@ -402,6 +454,11 @@ def main():
     _lib.load()
     dev = "cuda:0"
     B, H, T, D = 8, 12, 2048, 64
+    if args.calibrate_copy:
+        calibrate_copy(dev)
+    if args.once:
+        run_once(args.once, dev)
+        return
     if args.head_only:
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
                           for k, v in bench_head(args.steps, args.warmup, dev).items()}),
@@ -421,12 +478,6 @@ def main():
                           for k, v in bench_elementwise(args.steps, args.warmup, dev).items()}),
               flush=True)
         return
-    if args.calibrate_copy:
-        src = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
     torch.cuda.synchronize()
     a = bench_attention(B, H, T, D, args.steps, args.warmup, dev)
     bwd_achieved = a["bwd_flops"] / (a["bwd_kernel_ms"] * 1e-3) / 1e12

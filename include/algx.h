@@ -7,7 +7,9 @@
  * No entry point allocates device memory or synchronises with the host:
  * scratch memory is a caller-provided workspace whose size the matching
  * *_workspace_bytes() query reports. Calls on different streams/devices are
- * independent; the library holds no state besides the thread-local error text.
+ * independent. Library state: the thread-local error text and one
+ * process-wide timing probe (algx_set_probe, a benchmark diagnostic that is
+ * off unless armed); no entry point's results depend on either.
  *
  * Layouts are row-major as the reference passes them: attention tensors are
  * (B, H, T, D); the head takes hidden states (N, d) and the tied embedding
@@ -149,8 +151,10 @@ int32_t algx_attn_bwd(const void* q_s, const void* k, const void* v, const float
  * (N, V) logits. h: (N, d) and E: (V, d) in `dtype` (the reference casts E to
  * h's dtype, :168); targets int32 (N,); stat, zt float32 (N,).
  * scale: device float32 scalar g * (1 or n/c) / N (fused_head.py:251).
- * dh: (N, d) in dtype; dE: (V, d) float32. The MFMA kernels take bf16 (dtype
- * ALGX_BF16) hidden states with d % 8 == 0; V is arbitrary (ragged tail masked). */
+ * dh: (N, d) in dtype; dE: (V, d) float32. bf16 hidden states (ALGX_BF16,
+ * d % 8 == 0) run the MFMA kernels; float32 ones (ALGX_F32, any d) a float32
+ * path with float32 logits and dz, as the reference computes for float32 h.
+ * V is arbitrary (ragged tail masked). */
 int64_t algx_head_fwd_workspace_bytes(int32_t N, int32_t d, int32_t V, int32_t dtype);
 int32_t algx_head_fwd(const void* h, const void* E, const int32_t* targets, float* stat,
                       float* zt, void* workspace, int32_t N, int32_t d, int32_t V, int32_t kind,

@@ -63,8 +63,8 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert rc != 0 and b"multiple of 8" in lib.algx_last_error()
     rc = lib.algx_rms_norm_fwd(None, None, None, 4, 100, 0, 1e-5, None)
     assert rc != 0 and b"multiple of 8" in lib.algx_last_error()
-    rc = lib.algx_rms_norm_fwd(None, None, None, 4, 2048, 1, 1e-5, None)
-    assert rc != 0 and b"at most 1024" in lib.algx_last_error()
+    rc = lib.algx_rms_norm_fwd(None, None, None, 4, 2056, 1, 1e-5, None)
+    assert rc != 0 and b"at most 2048" in lib.algx_last_error()
     rc = lib.algx_rms_norm_bwd(None, None, None, None, None, None, 0, 64, 0, 1e-5, None)
     assert rc == 0
     g = ctypes.c_void_p(16)
@@ -130,8 +130,8 @@ def test_head_and_norm_validation_mirror_reference():
 def test_elementwise_validation():
     with pytest.raises(NotImplementedError, match="multiple of 8"):
         rms_norm(_t((4, 100)), None)
-    with pytest.raises(NotImplementedError, match="at most 1024"):
-        rms_norm(_t((4, 2048)), None)
+    with pytest.raises(NotImplementedError, match="at most 2048"):
+        rms_norm(_t((4, 2056)), None)
     with pytest.raises(ValueError, match="gain must have shape"):
         rms_norm(_t((4, 64)), torch.ones(32))
     with pytest.raises(ValueError, match="positive"):

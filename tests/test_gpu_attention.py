@@ -284,3 +284,166 @@ def test_fused_forward_equals_prepare_then_forward(tail):
     assert torch.equal(qs1, qs2)
     assert torch.equal(o1, o2)
     assert torch.equal(s1, s2)
+
+
+# Heads with a nonzero output gradient in the full-grid backward test: their
+# b*H + h fall on XCD slots 3, 5 and 7 (b*H + h mod 8) at H = 12 and H = 16.
+_GRAD_HEADS = ((0, 3), (2, 5), (6, 7))
+
+
+@pytest.mark.parametrize("H", [12, 16])
+def test_benchmark_shape_backward_selected_heads(H):
+    """The whole (8, H, 2048, 64) bf16 guarded grid runs forward and backward
+    (768 or 1024 backward workgroups, the float32 dQ atomics, the XCD head
+    map), with dO nonzero in three heads on different XCD slots: those heads'
+    o, dq, dk, dv match the oracle and every other head's gradients are
+    exactly zero. With dO dense instead, sum_keys dV = sum_queries dO for every
+    (b, h, d) (the weights of each query row sum to one)."""
+    B, T, D = 8, 2048, 64
+    shape = (B, H, T, D)
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    q = torch.randn(shape, device=DEV, generator=gen)
+    k = torch.randn(shape, device=DEV, generator=gen)
+    q = (q * torch.rsqrt((q * q).mean(-1, keepdim=True) + 1e-5)).bfloat16()
+    k = (k * torch.rsqrt((k * k).mean(-1, keepdim=True) + 1e-5)).bfloat16()
+    v = torch.randn(shape, device=DEV, generator=gen).bfloat16()
+    do_full = torch.randn(shape, device=DEV, generator=gen).bfloat16()
+    do = torch.zeros_like(do_full)
+    heads = list(_GRAD_HEADS)
+    assert sorted((b * H + h) % 8 for b, h in heads) == [3, 5, 7]
+    for b, h in heads:
+        do[b, h] = do_full[b, h]
+    kw = dict(kind="asinh", n=16, c=8.0, range_guard=True)
+    tq, tk, tv = (x.clone().requires_grad_(True) for x in (q, k, v))
+    o = flash_attention(tq, tk, tv, **kw)
+    dq, dk, dv = torch.autograd.grad(o, (tq, tk, tv), do)
+    torch.cuda.synchronize()
+    mask = torch.ones((B, H), dtype=torch.bool)
+    for b, h in heads:
+        mask[b, h] = False
+    for name, g in (("dq", dq), ("dk", dk), ("dv", dv)):
+        assert torch.count_nonzero(g[mask.to(DEV)]) == 0, name
+    for b, h in heads:
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        res = OA.flash_attention(to_np(q[sl]), to_np(k[sl]), to_np(v[sl]), None, dtype="bf16",
+                                 do=to_np(do[sl]), **kw)
+        assert res.in_range
+        assert_bf16(o[sl], res.o, what=f"o{b, h}")
+        for got, want, name in zip((dq, dk, dv), res.grads[:3], ("dq", "dk", "dv")):
+            assert_bf16(got[sl], want, what=f"{name}{b, h}")
+    # dense dO: column sums of dV equal those of dO, head by head
+    dv_full = torch.autograd.grad(flash_attention(tq, tk, tv, **kw), tv, do_full)[0]
+    lhs = dv_full.double().sum(2)
+    rhs = do_full.double().sum(2)
+    err = (lhs - rhs).abs().max().item()
+    assert err <= 2e-2 * rhs.abs().max().item() + 0.5, err
+    assert rel_l2(lhs, rhs) <= 5e-3
+
+
+def test_guarded_tail_at_benchmark_shape():
+    """Out-of-range inputs at (8, 12, 2048, 64): 1536 query tiles go through
+    the high-variant fallback grid of 512 workgroups, so each workgroup walks
+    three tiles (the grid-stride loop). One head against the oracle."""
+    B, H, T, D = 8, 12, 2048, 64
+    shape = (B, H, T, D)
+    q = torch.full(shape, math.sqrt(1000.0), dtype=torch.bfloat16, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(12)
+    v = torch.randn(shape, device=DEV, generator=gen).bfloat16()
+    do = torch.randn(shape, device=DEV, generator=gen).bfloat16()
+    kw = dict(kind="asinh", n=16, c=8.0, range_guard=True)
+    tq, tk, tv = (x.clone().requires_grad_(True) for x in (q, q, v))
+    o = flash_attention(tq, tk, tv, **kw)
+    dq, dk, dv = torch.autograd.grad(o, (tq, tk, tv), do)
+    torch.cuda.synchronize()
+    assert all(torch.isfinite(x.float()).all() for x in (o, dq, dk, dv))
+    for b, h in ((0, 0), (5, 7), (7, 11)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        res = OA.flash_attention(to_np(q[sl]), to_np(q[sl]), to_np(v[sl]), None, dtype="bf16",
+                                 do=to_np(do[sl]), **kw)
+        assert res.in_range is False
+        assert_bf16(o[sl], res.o, what=f"o{b, h}")
+        assert_bf16(dv[sl], res.grads[2], what=f"dv{b, h}")
+        # equal scores: dq, dk are differences of nearly equal bf16-rounded
+        # terms (test_flash_kernel_tpu.py:205-207): absolute check only
+        for got, want in ((dq, res.grads[0]), (dk, res.grads[1])):
+            assert np.abs(to_np(got[sl]) - want).max() <= 2e-2
+
+
+def test_bf16_clipping_vjp_is_zero_above_cap():
+    """test_flash_kernel_tpu.py:122-138 in bf16 through the MFMA kernels: every
+    score (and the sink) above the unguarded clamp of shift=False, n=16, T=256
+    (72.58) has a zero VJP."""
+    shape = (1, 1, 256, 64)
+    q = torch.full(shape, math.sqrt(1000), dtype=torch.bfloat16)
+    v, g = _rand(shape, 39, n=2)
+    got = _run(q, q.clone(), v, g, torch.full((1,), 1000.0), kind="asinh", n=16, c=8.0,
+               block=128, shift=False, range_guard=False)
+    for x in (got[1], got[2], got[4]):
+        assert np.all(x == 0)
+    assert np.isfinite(got[0]).all() and np.isfinite(got[3]).all()
+
+
+@pytest.mark.parametrize("with_sink", [False, True])
+def test_bf16_partly_clipped_scores_match_oracle(with_sink):
+    """bf16, shift=False, unguarded, T=256: q, k ~ 20 N(0,1) puts a share of
+    the scores above the clamp (72.58) and the rest below it, so the MFMA
+    backward's clamp kink (zero score gradient at and above the clamp) and
+    the clamped weights meet ordinary ones in the same tiles."""
+    shape = (2, 2, 256, 64)
+    q, k, v, g = _rand(shape, 41)
+    q, k = ((x.float() * 20).bfloat16() for x in (q, k))
+    qs = q.float() / 64.0
+    s = qs @ k.float().transpose(-1, -2)
+    frac = (s > 72.58).float().tril().sum() / torch.ones_like(s).tril().sum()
+    assert 0.01 < frac.item() < 0.5, frac.item()
+    sink = torch.tensor([0.5, 1000.0]).reshape(1, 2, 1, 1) if with_sink else None
+    kw = dict(kind="asinh", n=16, c=8.0, shift=False, range_guard=False)
+    got = _run(q, k, v, g, sink, block=128, **kw)
+    want, _ = _oracle(q, k, v, g, sink, "bf16", **kw)
+    for a, b, nm in zip(got, want, ("o", "dq", "dk", "dv", "dsink")):
+        if a is None:
+            continue
+        if nm == "dsink":
+            assert np.abs(a - b).max() <= 1e-2 * max(1.0, np.abs(b).max()), (a, b)
+            continue
+        assert_bf16(a, b, what=nm)
+
+
+@pytest.mark.parametrize("kind,shift", [("asinh", False), ("asinh", True), ("softmax", True)])
+def test_precise_output_in_every_mode(kind, shift):
+    """A C-ABI caller may ask for the float32 output with any variant: the MFMA
+    forward writes o_precise in every mode (o is its bf16 rounding), and the
+    backward's di read from it gives the gradients of the bf16 residual to
+    within bf16 accuracy."""
+    from algebraic_amd.kernels.flash import _c_variant, make_variant
+
+    B, H, T, D = 1, 2, 256, 64
+    q, k, v, do = (x.to(DEV) for x in _rand((B, H, T, D), 93, n=4))
+    var = make_variant(kind, 16, 8.0, seq_len=T)
+    if kind == "asinh":
+        var = var._replace(shift=shift, inv_stat=not shift, bounded_scores=not shift)
+    st = _lib.stream()
+    outs = []
+    for precise in (1, 0):
+        lo = _c_variant(var._replace(precise_output=bool(precise)))
+        q_s = (q.float() * (1.0 / (8.0 * math.sqrt(D)) if kind == "asinh" else
+                            1.0 / math.sqrt(D))).bfloat16()
+        o = torch.empty_like(q)
+        o_precise = torch.full(q.shape, float("nan"), dtype=torch.float32, device=DEV)
+        stat = torch.empty((B, H, T), dtype=torch.float32, device=DEV)
+        _lib.call("algx_attn_fwd", _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), None, _lib.ptr(o),
+                  _lib.ptr(o_precise), _lib.ptr(stat), B, H, T, D, _lib.BF16, lo, None, None, st)
+        dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+        ws = torch.empty(_lib.query("algx_attn_bwd_workspace_bytes", B, H, T, D),
+                         dtype=torch.uint8, device=DEV)
+        _lib.call("algx_attn_bwd", _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), None, _lib.ptr(o),
+                  _lib.ptr(o_precise), _lib.ptr(stat), _lib.ptr(do), _lib.ptr(dq), _lib.ptr(dk),
+                  _lib.ptr(dv), None, _lib.ptr(ws), B, H, T, D, _lib.BF16, 1.0, lo, None, None, st)
+        torch.cuda.synchronize()
+        if precise:
+            assert torch.isfinite(o_precise).all()
+            assert torch.equal(o_precise.bfloat16(), o)
+        outs.append((dq, dk, dv))
+    for a, b in zip(*outs):
+        assert torch.isfinite(a.float()).all()
+        assert rel_l2(a, b) <= 5e-3

@@ -33,10 +33,12 @@ def _randn(rng, shape, dtype, scale=1.0):
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("with_gain", [False, True])
 @pytest.mark.parametrize("rows,D", [(1, 8), (37, 64), (129, 776), (300, 768), (64, 1024),
-                                    (5, 1016)])
+                                    (5, 1016), (40, 1536), (9, 1288), (3, 2048)])
 def test_rms_norm_output_and_vjp(dtype, with_gain, rows, D):
-    """Ragged widths (776 = 97 bf16 chunks, 1016 = 254 f32 chunks) leave lanes
-    idle in a row's last chunk; row 0 is zero (tau = eps^-1/2, dx = tau dy)."""
+    """Ragged widths (776 = 97 bf16 chunks, 1016 = 254 f32 chunks, 1288 =
+    322 f32 chunks) leave lanes idle in a row's last chunk; 1536 is the 1b
+    preset's d_model and 2048 the widest row; row 0 is zero (tau = eps^-1/2,
+    dx = tau dy)."""
     if D % (8 if dtype == "bf16" else 4):
         pytest.skip("width not a multiple of the vector")
     rng = np.random.default_rng(1000 + rows + D)

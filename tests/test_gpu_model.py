@@ -90,6 +90,7 @@ def _run(cfg, seed=0):
 @pytest.mark.parametrize("preset", ["algebraic", "standard"])
 @pytest.mark.parametrize("dtype,head_impl,grad_tol,obj_tol", [
     ("float32", "dense", 1e-4, 1e-5),
+    ("float32", "fused", 1e-4, 1e-5),
     ("bfloat16", "fused", 3e-2, 1e-2),
 ])
 def test_small_model_matches_oracle(preset, dtype, head_impl, grad_tol, obj_tol, head_dim):

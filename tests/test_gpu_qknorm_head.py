@@ -114,6 +114,26 @@ def test_production_head_tiles_at_model_widths(width):
     assert rel_l2(got[2], dh) < 0.01 and rel_l2(got[3], de) < 0.01
 
 
+@pytest.mark.parametrize("kind,n,c", [("alg_ce", 8, 2.0), ("alg_ce", 16, 16.0), ("ce", 16, 16.0)])
+@pytest.mark.parametrize("N,d,V", [(512, 96, 4096), (300, 100, 1000), (64, 768, 50304)])
+def test_fused_head_float32_hidden_states(kind, n, c, N, d, V):
+    """float32 h: the embedding is cast to float32 and the logits, dz, dh and
+    dE are float32 (fused_head.py:160-216 with h.dtype = float32), so the
+    outputs meet the float32 tolerance against the float64 oracle. Ragged
+    token, vocabulary and width extents (d = 100 is no multiple of 8)."""
+    rng = np.random.default_rng(N + d)
+    h = torch.from_numpy(rng.standard_normal((N, d)).astype(np.float32))
+    e = torch.from_numpy((rng.standard_normal((V, d)) * 0.15).astype(np.float32))
+    t = torch.from_numpy(rng.integers(0, V, N).astype(np.int64))
+    got = _head_run(h, e, t, kind=kind, n=n, c=c, block_n=N)
+    (obj, tel), (dh, de) = OH.fused_head(to_np(h), to_np(e), to_np(t), kind=kind, n=n, c=c,
+                                         dtype="f32", g_obj=1.0)
+    assert abs(got[0] - obj) <= 1e-5 * abs(obj) + 1e-7
+    assert_f32(got[1], tel, what="telemetry")
+    assert_f32(got[2], dh, what="dh")
+    assert_f32(got[3], de, what="dE")
+
+
 def test_fused_head_alg_gradient_is_log_loss_gradient():
     """The alg_ce VJP equals the exact NLL gradient of log_softmax(n asinh(z/c))."""
     h, e, t = _head_inputs(256, 128, 4096, 9, 0.3)
