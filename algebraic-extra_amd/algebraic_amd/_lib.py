@@ -47,6 +47,8 @@ SIGNATURES = {
     "algx_attn_forward_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "algx_attn_forward": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32,
                                  _i32, _f32, _f32, _f32, _VP, _VP, _p]),
+    "algx_attn_forward_noalloc": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32,
+                                         _i32, _i32, _f32, _f32, _f32, _VP, _VP, _p]),
     "algx_attn_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "algx_attn_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,
                              _i32, _i32, _i32, _f32, _VP, _VP, _p, _p]),

@@ -6,6 +6,7 @@
 // returns at once. Either way this mirrors lax.cond(in_range, low, high) of
 // flash.py:853-856 without a host round trip.
 #include <cstdlib>
+#include <mutex>
 
 #include "attn_aux.h"
 
@@ -29,6 +30,35 @@ int32_t to_kvar(const algx_attn_variant* v, KVariant& out, const char* which) {
   out.precise = v->precise_output != 0;
   out.clamp = v->clamp;
   out.slope = v->kind == ALGX_ASINH ? (float)v->n : 1.0f;
+  return 0;
+}
+
+// Scratch of algx_attn_forward_noalloc: the guard's partial maxima, one
+// triple per forward workgroup, at most kNoAllocParts workgroups (768 KiB).
+// Each GPU the library runs on holds its own copy until the process ends.
+constexpr int64_t kNoAllocParts = 1 << 16;
+static __device__ __align__(256) float scratch[3 * kNoAllocParts];
+
+// Device address of `scratch` on the current device, looked up once per
+// device (the host-side name of a __device__ array is not its address).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+int32_t scratch_on_current_device(float** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail("attn_forward_noalloc: no current device");
+  if (dev < 0 || dev >= kMaxDevices) return fail("attn_forward_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(std::string("attn_forward_noalloc: hipGetSymbolAddress(scratch): ") +
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = (float*)p;
+  }
+  *out = g_scratch_ptr[dev];
   return 0;
 }
 
@@ -193,4 +223,26 @@ extern "C" int32_t algx_attn_bwd(const void* q, const void* k, const void* v, co
     return launch_bwd_generic(q, k, v, stat, di, dout, dq, dk, dv, B, H, T, D, dtype, q_scale, kh,
                               guard, 0, s);
   return 0;
+}
+
+// algx_attn_forward with the guard partials in the library's per-device
+// scratch array instead of a caller workspace: no allocation of any kind.
+extern "C" int32_t algx_attn_forward_noalloc(const void* q, const void* k, const void* v,
+                                             const float* sink, void* q_s, void* o,
+                                             float* o_precise, float* stat, int32_t* guard,
+                                             int32_t B, int32_t H, int32_t T, int32_t D,
+                                             int32_t dtype, float q_scale, float bound,
+                                             float vmax, const algx_attn_variant* low,
+                                             const algx_attn_variant* high, void* stream) {
+  if (int32_t rc = check_shape(B, H, T, D, dtype)) return rc;
+  float* part = nullptr;
+  if (guard != nullptr && (int64_t)B * H * T > 0 && mfma_supported(T, D, dtype) &&
+      !force_generic()) {
+    if (fwd_fused_partials(B, H, T) > kNoAllocParts)
+      return fail("attn_forward_noalloc: B * H * T / 128 exceeds the scratch limit of 65536 "
+                  "forward workgroups; use algx_attn_forward with a workspace");
+    if (int32_t rc = scratch_on_current_device(&part)) return rc;
+  }
+  return algx_attn_forward(q, k, v, sink, q_s, o, o_precise, stat, guard, part, B, H, T, D,
+                           dtype, q_scale, bound, vmax, low, high, stream);
 }

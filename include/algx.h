@@ -133,6 +133,21 @@ int32_t algx_attn_forward(const void* q, const void* k, const void* v, const flo
                           const algx_attn_variant* low, const algx_attn_variant* high,
                           void* stream);
 
+/* No counterpart in the reference: algx_attn_forward for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). Same arguments and results, no workspace: the guard's partial
+ * maxima live in a static per-device scratch array of the library (768 KiB,
+ * held by each GPU the library runs on until the process ends), so
+ * B * H * T / 128 may not exceed 65536 on the MFMA shapes (a larger call
+ * returns an error). Every call on one GPU shares that array: calls that
+ * overlap on one GPU (concurrent streams) race. */
+int32_t algx_attn_forward_noalloc(const void* q, const void* k, const void* v, const float* sink,
+                                  void* q_s, void* o, float* o_precise, float* stat,
+                                  int32_t* guard, int32_t B, int32_t H, int32_t T, int32_t D,
+                                  int32_t dtype, float q_scale, float bound, float vmax,
+                                  const algx_attn_variant* low, const algx_attn_variant* high,
+                                  void* stream);
+
 int64_t algx_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t T, int32_t D);
 /* dq is w.r.t. the unscaled q: dq = cast(cast(dq_s) * q_scale) as autodiff of
  * flash.py:833 gives; dsink (H,) float32 is w.r.t. the kernel-unit sink
