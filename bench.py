@@ -343,15 +343,16 @@ def bench_model(preset, steps, warmup, dev, B=8, T=2048, V=50304, remat=True, op
     return out
 
 
-def traffic_bytes():
-    """HBM bytes per attention-backward launch measured by rocprofv3 --pmc
-    (FETCH_SIZE + WRITE_SIZE, scaled by a 256 MiB copy), when that summary
-    has been recorded in profiles/attn_bwd_traffic.json; else None."""
+def bwd_counters():
+    """Counter figures of the attention-backward kernel recorded from
+    rocprofv3 --pmc runs in profiles/attn_bwd_traffic.json (HBM bytes per
+    launch from FETCH_SIZE + WRITE_SIZE, MFMA / VALU / LDS busy fractions);
+    empty when that summary is absent."""
     path = os.path.join(ROOT, "profiles", "attn_bwd_traffic.json")
     if not os.path.exists(path):
-        return None
+        return {}
     with open(path) as f:
-        return json.load(f).get("bytes_per_launch")
+        return json.load(f)
 
 
 def cpu_baseline(B, H, T, D, heads=None, runs=6):
@@ -500,7 +501,9 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "attention backward (bwd_mfma_kernel)",
                      "achieved": round(bwd_achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(bwd_achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic_bytes(),
+                     "traffic": bwd_counters().get("bytes_per_launch"),
+                     "mfma_busy": bwd_counters().get("mfma_busy"),
+                     "valu_busy": bwd_counters().get("valu_busy"),
                      "flops_per_launch": a["bwd_flops"],
                      "avg_launch_ms": round(a["bwd_kernel_ms"], 4)},
         "step_frac_of_peak": round(a["tflops"] / PEAK_BF16_TFLOPS, 4),
