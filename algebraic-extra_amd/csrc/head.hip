@@ -482,18 +482,35 @@ __device__ __forceinline__ void gemm_job(const GemmJob& jb, int tile, bf16* As, 
     }
 }
 
+// XCD-aware tile order of a grouped GEMM: workgroups are dealt to the 8 XCDs
+// round-robin by index, so the tiles_n output tiles that share one row block
+// of A (one dz block) go to indices 8 apart, i.e. to one XCD and its L2, and
+// run at about the same time. Index `b` counts from a multiple of 8; a
+// trailing partial group keeps the plain order.
+__device__ __forceinline__ int xcd_tile(int b, int ntiles, int tiles_n) {
+  const int grp = 8 * tiles_n;
+  const int full = ntiles / grp * grp;
+  if (b >= full) return b;
+  const int r = b % grp;
+  return ((b / grp) * 8 + (r & 7)) * tiles_n + (r >> 3);
+}
+
 // The backward's two products of a token chunk in one launch (the long-K dh
-// tiles first): dh[t][c] = sum_v dz[t][v] E[v][c] for blocks [0, n_dh), then
-// dE[v][c] (+)= sum_t dz[t][v] h[t][c].
+// tiles first): dh[t][c] = sum_v dz[t][v] E[v][c] in the first dh_slots
+// workgroups (n_dh tiles; dh_slots is n_dh rounded up to a multiple of 8),
+// then dE[v][c] (+)= sum_t dz[t][v] h[t][c].
 template <bool ACCUM>
-__global__ __launch_bounds__(kThreads) void head_grad_kernel(GemmJob dh, GemmJob de, int n_dh) {
+__global__ __launch_bounds__(kThreads) void head_grad_kernel(GemmJob dh, GemmJob de, int n_dh,
+                                                             int dh_slots, int n_de) {
   __shared__ __attribute__((aligned(16))) bf16 As[2 * kStageElems];
   __shared__ __attribute__((aligned(16))) bf16 Bs[2 * kStageElems];
   const int b = blockIdx.x;
-  if (b < n_dh)
-    gemm_job<true, false, bf16, false>(dh, b, As, Bs, threadIdx.x);
-  else
-    gemm_job<false, false, float, ACCUM>(de, b - n_dh, As, Bs, threadIdx.x);
+  if (b < dh_slots) {
+    if (b < n_dh) gemm_job<true, false, bf16, false>(dh, xcd_tile(b, n_dh, dh.tiles_n), As, Bs, threadIdx.x);
+  } else {
+    gemm_job<false, false, float, ACCUM>(de, xcd_tile(b - dh_slots, n_de, de.tiles_n), As, Bs,
+                                         threadIdx.x);
+  }
 }
 
 int64_t vpad_of(int V) { return ((int64_t)V + BM - 1) / BM * BM; }
@@ -644,8 +661,9 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
                       dE, (int64_t)d, V, d, tn};
     const int n_dh = ((ntok + BM - 1) / BM) * tn;
     const int n_de = ((V + BM - 1) / BM) * tn;
+    const int dh_slots = (n_dh + 7) / 8 * 8;
     launch_k(probe_for(ALGX_PROBE_HEAD_DE), tok0 == 0 ? head_grad_kernel<false> : head_grad_kernel<true>,
-             dim3(n_dh + n_de), dim3(kThreads), s, jdh, jde, n_dh);
+             dim3(dh_slots + n_de), dim3(kThreads), s, jdh, jde, n_dh, dh_slots, n_de);
     if (int32_t rc = check_launch("head_grad")) return rc;
   }
   return 0;
