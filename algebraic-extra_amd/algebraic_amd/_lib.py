@@ -39,6 +39,10 @@ SIGNATURES = {
     "algx_qknorm_fwd": (_i32, [_p, _p, _p, _i64, _i32, _i32, _f32, _p]),
     "algx_qknorm_bwd_workspace_bytes": (_i64, [_i64, _i32, _i32]),
     "algx_qknorm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _f32, _p]),
+    "algx_qknorm_pair_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _f32, _p]),
+    "algx_qknorm_pair_bwd_workspace_bytes": (_i64, [_i64, _i32, _i32]),
+    "algx_qknorm_pair_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32,
+                                    _f32, _p]),
     "algx_attn_guard_words": (_i32, []),
     "algx_attn_prepare": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32,
                                  _f32, _f32, _p]),

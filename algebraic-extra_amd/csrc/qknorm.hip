@@ -9,6 +9,11 @@
 // xor-shuffles inside the LPR-lane group. dgain is reduced per block into a
 // workspace row and summed by a finishing kernel with one block per column
 // (deterministic).
+//
+// One launch covers one tensor or a pair (the attention's q and k, each with
+// its own gain): the first nb0 blocks stream tensor 0, the rest tensor 1, so
+// the pair moves as one 134 MB (forward) / 201 MB (backward) stream instead of
+// two half-size ones.
 #include "common.h"
 
 namespace algx {
@@ -29,21 +34,34 @@ template <int LPR> __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Tensors of one launch: blocks [0, nb0) take tensor 0, [nb0, gridDim.x)
+// tensor 1 (nb0 == gridDim.x for a single tensor).
 template <typename T>
-__global__ __launch_bounds__(kThreads) void qknorm_fwd_kernel(const T* __restrict__ x,
-                                                              const float* __restrict__ gain,
-                                                              T* __restrict__ y, int64_t rows,
+struct NormPair {
+  const T* x[2];
+  const float* gain[2];
+  const T* dy[2];
+  T* out[2];  // y (forward) or dx (backward)
+  int nb0;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void qknorm_fwd_kernel(NormPair<T> P, int64_t rows,
                                                               float eps) {
   typedef typename Vec<T>::type VT;
   constexpr int EPL = Vec<T>::n;
   constexpr int LPR = kD / EPL;
   constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63, sub = lane % LPR, rw = lane / LPR;
+  const int t = blockIdx.x >= P.nb0 ? 1 : 0;
+  const int blk = blockIdx.x - t * P.nb0, nblk = t ? gridDim.x - P.nb0 : P.nb0;
+  const T* __restrict__ x = P.x[t];
+  T* __restrict__ y = P.out[t];
   float g[EPL];
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) g[i] = gain[sub * EPL + i];
-  const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  const int64_t stride = (int64_t)gridDim.x * (kThreads / 64) * RPW;
+  for (int i = 0; i < EPL; ++i) g[i] = P.gain[t][sub * EPL + i];
+  const int64_t wave = (int64_t)blk * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t stride = (int64_t)nblk * (kThreads / 64) * RPW;
   for (int64_t row = wave * RPW + rw; row < rows; row += stride) {
     VT in = *reinterpret_cast<const VT*>(x + row * kD + sub * EPL);
     float xs[EPL];
@@ -62,23 +80,29 @@ __global__ __launch_bounds__(kThreads) void qknorm_fwd_kernel(const T* __restric
   }
 }
 
+// partial: one dgain row per block (tensor 0's blocks first).
 template <typename T>
-__global__ __launch_bounds__(kThreads) void qknorm_bwd_kernel(
-    const T* __restrict__ x, const float* __restrict__ gain, const T* __restrict__ dy,
-    T* __restrict__ dx, float* __restrict__ partial, int64_t rows, float eps) {
+__global__ __launch_bounds__(kThreads) void qknorm_bwd_kernel(NormPair<T> P,
+                                                              float* __restrict__ partial,
+                                                              int64_t rows, float eps) {
   typedef typename Vec<T>::type VT;
   constexpr int EPL = Vec<T>::n;
   constexpr int LPR = kD / EPL;
   constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63, sub = lane % LPR, rw = lane / LPR;
+  const int t = blockIdx.x >= P.nb0 ? 1 : 0;
+  const int blk = blockIdx.x - t * P.nb0, nblk = t ? gridDim.x - P.nb0 : P.nb0;
+  const T* __restrict__ x = P.x[t];
+  const T* __restrict__ dy = P.dy[t];
+  T* __restrict__ dx = P.out[t];
   float g[EPL], dg[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
-    g[i] = gain[sub * EPL + i];
+    g[i] = P.gain[t][sub * EPL + i];
     dg[i] = 0.0f;
   }
-  const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  const int64_t stride = (int64_t)gridDim.x * (kThreads / 64) * RPW;
+  const int64_t wave = (int64_t)blk * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t stride = (int64_t)nblk * (kThreads / 64) * RPW;
   for (int64_t row = wave * RPW + rw; row < rows; row += stride) {
     VT xin = *reinterpret_cast<const VT*>(x + row * kD + sub * EPL);
     VT din = *reinterpret_cast<const VT*>(dy + row * kD + sub * EPL);
@@ -125,14 +149,21 @@ __global__ __launch_bounds__(kThreads) void qknorm_bwd_kernel(
   }
 }
 
+// Block c of tensor t (blockIdx.x = 64 t + c) finishes dgain column c of
+// tensor t from that tensor's nblocks partial rows.
 __global__ __launch_bounds__(kThreads) void qknorm_gain_finish(const float* __restrict__ partial,
-                                                               int nblocks,
-                                                               float* __restrict__ dgain) {
+                                                               int nblocks0, int nblocks1,
+                                                               float* __restrict__ dgain0,
+                                                               float* __restrict__ dgain1) {
   // One block per gain column: every thread sums a strided slice of the block
   // partials with independent loads in flight, then a fixed-order tree in LDS
   // finishes the column (deterministic for a given grid).
   __shared__ float red[kThreads];
-  const int col = blockIdx.x;
+  const int t = blockIdx.x >= kD ? 1 : 0;
+  const int col = blockIdx.x - t * kD;
+  const int nblocks = t ? nblocks1 : nblocks0;
+  float* __restrict__ dgain = t ? dgain1 : dgain0;
+  partial += t ? (int64_t)nblocks0 * kD : 0;
   float s0 = 0.0f, s1 = 0.0f;
   int b = threadIdx.x;
   for (; b + kThreads < nblocks; b += 2 * kThreads) {
@@ -170,6 +201,57 @@ int32_t check_args(const void* x, const float* gain, int64_t rows, int32_t D, in
   return 0;
 }
 
+
+template <typename T>
+int32_t launch_fwd(const NormPair<T>& P, int nb, int64_t rows, float eps, hipStream_t s) {
+  launch_k(probe_for(ALGX_PROBE_QKNORM_FWD), qknorm_fwd_kernel<T>, dim3(nb), dim3(kThreads), s,
+           P, rows, eps);
+  return check_launch("qknorm_fwd");
+}
+
+template <typename T>
+int32_t launch_bwd(const NormPair<T>& P, int nb, float* partial, float* dgain0, float* dgain1,
+                   int64_t rows, float eps, hipStream_t s) {
+  launch_k(probe_for(ALGX_PROBE_QKNORM_BWD), qknorm_bwd_kernel<T>, dim3(nb), dim3(kThreads), s,
+           P, partial, rows, eps);
+  if (int32_t rc = check_launch("qknorm_bwd")) return rc;
+  const bool pair = nb > P.nb0;
+  qknorm_gain_finish<<<pair ? 2 * kD : kD, kThreads, 0, s>>>(partial, P.nb0, nb - P.nb0, dgain0,
+                                                             dgain1);
+  return check_launch("qknorm_gain_finish");
+}
+
+// Forward over one (x1 == nullptr) or two tensors of `rows` rows each.
+int32_t norm_fwd(const void* x0, const void* x1, const float* g0, const float* g1, void* y0,
+                 void* y1, int64_t rows, int32_t dtype, float eps, hipStream_t s) {
+  const int nb0 = blocks_for(rows, dtype);
+  const int nb = x1 != nullptr ? 2 * nb0 : nb0;
+  if (dtype == ALGX_BF16) {
+    const NormPair<bf16> P{{(const bf16*)x0, (const bf16*)x1}, {g0, g1}, {nullptr, nullptr},
+                           {(bf16*)y0, (bf16*)y1}, nb0};
+    return launch_fwd(P, nb, rows, eps, s);
+  }
+  const NormPair<float> P{{(const float*)x0, (const float*)x1}, {g0, g1}, {nullptr, nullptr},
+                          {(float*)y0, (float*)y1}, nb0};
+  return launch_fwd(P, nb, rows, eps, s);
+}
+
+int32_t norm_bwd(const void* x0, const void* x1, const float* g0, const float* g1,
+                 const void* dy0, const void* dy1, void* dx0, void* dx1, float* dg0, float* dg1,
+                 float* partial, int64_t rows, int32_t dtype, float eps, hipStream_t s) {
+  const int nb0 = blocks_for(rows, dtype);
+  const int nb = x1 != nullptr ? 2 * nb0 : nb0;
+  if (dtype == ALGX_BF16) {
+    const NormPair<bf16> P{{(const bf16*)x0, (const bf16*)x1}, {g0, g1},
+                           {(const bf16*)dy0, (const bf16*)dy1}, {(bf16*)dx0, (bf16*)dx1}, nb0};
+    return launch_bwd(P, nb, partial, dg0, dg1, rows, eps, s);
+  }
+  const NormPair<float> P{{(const float*)x0, (const float*)x1}, {g0, g1},
+                          {(const float*)dy0, (const float*)dy1}, {(float*)dx0, (float*)dx1},
+                          nb0};
+  return launch_bwd(P, nb, partial, dg0, dg1, rows, eps, s);
+}
+
 }  // namespace
 }  // namespace algx
 
@@ -180,16 +262,7 @@ extern "C" int32_t algx_qknorm_fwd(const void* x, const float* gain, void* y, in
   if (int32_t rc = check_args(x, gain, rows, D, dtype, eps)) return rc;
   if (rows == 0) return 0;
   if (y == nullptr) return fail("qknorm: null output");
-  hipStream_t s = (hipStream_t)stream;
-  const int nb = blocks_for(rows, dtype);
-  const Probe probe = probe_for(ALGX_PROBE_QKNORM_FWD);
-  if (dtype == ALGX_BF16)
-    launch_k(probe, qknorm_fwd_kernel<bf16>, dim3(nb), dim3(kThreads), s, (const bf16*)x, gain,
-             (bf16*)y, rows, eps);
-  else
-    launch_k(probe, qknorm_fwd_kernel<float>, dim3(nb), dim3(kThreads), s, (const float*)x, gain,
-             (float*)y, rows, eps);
-  return check_launch("qknorm_fwd");
+  return norm_fwd(x, nullptr, gain, nullptr, y, nullptr, rows, dtype, eps, (hipStream_t)stream);
 }
 
 extern "C" int64_t algx_qknorm_bwd_workspace_bytes(int64_t rows, int32_t D, int32_t dtype) {
@@ -203,22 +276,43 @@ extern "C" int32_t algx_qknorm_bwd(const void* x, const float* gain, const void*
   if (int32_t rc = check_args(x, gain, rows, D, dtype, eps)) return rc;
   if (dgain == nullptr || workspace == nullptr) return fail("qknorm: null dgain/workspace");
   hipStream_t s = (hipStream_t)stream;
-  if (rows == 0) {
-    return fill_f32(dgain, kD, 0.0f, s);
-  }
+  if (rows == 0) return fill_f32(dgain, kD, 0.0f, s);
   if (dy == nullptr || dx == nullptr) return fail("qknorm: null dy/dx");
-  const int nb = blocks_for(rows, dtype);
-  float* partial = (float*)workspace;
-  {
-    const Probe probe = probe_for(ALGX_PROBE_QKNORM_BWD);
-    if (dtype == ALGX_BF16)
-      launch_k(probe, qknorm_bwd_kernel<bf16>, dim3(nb), dim3(kThreads), s, (const bf16*)x, gain,
-               (const bf16*)dy, (bf16*)dx, partial, rows, eps);
-    else
-      launch_k(probe, qknorm_bwd_kernel<float>, dim3(nb), dim3(kThreads), s, (const float*)x,
-               gain, (const float*)dy, (float*)dx, partial, rows, eps);
+  return norm_bwd(x, nullptr, gain, nullptr, dy, nullptr, dx, nullptr, dgain, nullptr,
+                  (float*)workspace, rows, dtype, eps, s);
+}
+
+extern "C" int32_t algx_qknorm_pair_fwd(const void* xq, const void* xk, const float* gain_q,
+                                        const float* gain_k, void* yq, void* yk, int64_t rows,
+                                        int32_t D, int32_t dtype, float eps, void* stream) {
+  if (int32_t rc = check_args(xq, gain_q, rows, D, dtype, eps)) return rc;
+  if (int32_t rc = check_args(xk, gain_k, rows, D, dtype, eps)) return rc;
+  if (rows == 0) return 0;
+  if (yq == nullptr || yk == nullptr) return fail("qknorm: null output");
+  return norm_fwd(xq, xk, gain_q, gain_k, yq, yk, rows, dtype, eps, (hipStream_t)stream);
+}
+
+extern "C" int64_t algx_qknorm_pair_bwd_workspace_bytes(int64_t rows, int32_t D, int32_t dtype) {
+  (void)D;
+  return 2 * (int64_t)blocks_for(rows, dtype) * kD * sizeof(float);
+}
+
+extern "C" int32_t algx_qknorm_pair_bwd(const void* xq, const void* xk, const float* gain_q,
+                                        const float* gain_k, const void* dyq, const void* dyk,
+                                        void* dxq, void* dxk, float* dgain_q, float* dgain_k,
+                                        void* workspace, int64_t rows, int32_t D, int32_t dtype,
+                                        float eps, void* stream) {
+  if (int32_t rc = check_args(xq, gain_q, rows, D, dtype, eps)) return rc;
+  if (int32_t rc = check_args(xk, gain_k, rows, D, dtype, eps)) return rc;
+  if (dgain_q == nullptr || dgain_k == nullptr || workspace == nullptr)
+    return fail("qknorm: null dgain/workspace");
+  hipStream_t s = (hipStream_t)stream;
+  if (rows == 0) {
+    if (int32_t rc = fill_f32(dgain_q, kD, 0.0f, s)) return rc;
+    return fill_f32(dgain_k, kD, 0.0f, s);
   }
-  if (int32_t rc = check_launch("qknorm_bwd")) return rc;
-  qknorm_gain_finish<<<kD, kThreads, 0, s>>>(partial, nb, dgain);
-  return check_launch("qknorm_gain_finish");
+  if (dyq == nullptr || dyk == nullptr || dxq == nullptr || dxk == nullptr)
+    return fail("qknorm: null dy/dx");
+  return norm_bwd(xq, xk, gain_q, gain_k, dyq, dyk, dxq, dxk, dgain_q, dgain_k,
+                  (float*)workspace, rows, dtype, eps, s);
 }

@@ -198,8 +198,11 @@ def library_gemm_rates(h, E, iters=10):
 
 
 def bench_qknorm(steps, warmup, dev):
+    """QK-norm over the attention's q and k ([8, 2048, 16, 64] bf16 each) in
+    one launch each way (qk_rms_norm_pair); the per-tensor calls are timed
+    beside it."""
     import torch
-    from algebraic_amd.kernels import qk_rms_norm
+    from algebraic_amd.kernels import qk_rms_norm, qk_rms_norm_pair
     gen = torch.Generator(device=dev).manual_seed(3)
     shape = (8, 2048, 16, 64)
     xs = [torch.randn(shape, device=dev, generator=gen).bfloat16().requires_grad_(True)
@@ -208,23 +211,31 @@ def bench_qknorm(steps, warmup, dev):
              for _ in range(2)]
     dys = [torch.randn(shape, device=dev, generator=gen).bfloat16() for _ in range(2)]
 
-    def step():
+    def pair_step():
+        yq, yk = qk_rms_norm_pair(xs[0], xs[1], gains[0], gains[1])
+        torch.autograd.grad((yq, yk), (xs[0], xs[1], gains[0], gains[1]), dys)
+
+    def single_step():
         for x, g, dy in zip(xs, gains, dys):
             torch.autograd.grad(qk_rms_norm(x, g), (x, g), dy)
 
     fp, bp = Probe("qknorm_fwd", steps), Probe("qknorm_bwd", steps)
-    time_steps(step, steps, warmup, fp)
-    time_steps(step, steps, 1, bp)
-    elems = xs[0].numel()
-    # the probe brackets one call; the second tensor's call re-arms nothing, so
-    # each pair holds the last (k) call of its step
+    time_steps(pair_step, steps, warmup, fp)
+    time_steps(pair_step, steps, 1, bp)
+    sfp, sbp = Probe("qknorm_fwd", steps), Probe("qknorm_bwd", steps)
+    time_steps(single_step, steps, warmup, sfp, settle_s=0.0)
+    time_steps(single_step, steps, 1, sbp, settle_s=0.0)
+    elems = 2 * xs[0].numel()
+    # Each probe brackets the row kernel of one launch (the dgain finish is a
+    # separate 128-block launch); the per-tensor probe holds the k call.
     fwd_bytes, bwd_bytes = elems * 4, elems * 6
     f_ms, b_ms = fp.mean_ms(), bp.mean_ms()
-    return {"workload": "q,k each [8,2048,16,64] bf16, D=64 rows",
+    return {"workload": "q,k each [8,2048,16,64] bf16, D=64 rows, one launch for both",
             "fwd_us": f_ms * 1e3, "fwd_gbs": fwd_bytes / f_ms / 1e6,
             "bwd_us": b_ms * 1e3, "bwd_gbs": bwd_bytes / b_ms / 1e6,
             "fwd_frac": fwd_bytes / f_ms / 1e6 / PEAK_HBM_GBS,
-            "bwd_frac": bwd_bytes / b_ms / 1e6 / PEAK_HBM_GBS}
+            "bwd_frac": bwd_bytes / b_ms / 1e6 / PEAK_HBM_GBS,
+            "per_tensor_fwd_us": sfp.mean_ms() * 1e3, "per_tensor_bwd_us": sbp.mean_ms() * 1e3}
 
 
 def bench_elementwise(steps, warmup, dev):
@@ -407,7 +418,7 @@ def run_once(which, dev, steps=3):
             obj, _ = fused_head(h, E, t, kind="alg_ce", n=8, c=2.0)
             torch.autograd.grad(obj, (h, E))
     else:
-        from algebraic_amd.kernels import qk_rms_norm
+        from algebraic_amd.kernels import qk_rms_norm_pair
         gen = torch.Generator(device=dev).manual_seed(3)
         shape = (8, 2048, 16, 64)
         xs = [torch.randn(shape, device=dev, generator=gen).bfloat16().requires_grad_(True)
@@ -416,8 +427,8 @@ def run_once(which, dev, steps=3):
                  for _ in range(2)]
         dys = [torch.randn(shape, device=dev, generator=gen).bfloat16() for _ in range(2)]
         for _ in range(steps):
-            for x, g, dy in zip(xs, gains, dys):
-                torch.autograd.grad(qk_rms_norm(x, g), (x, g), dy)
+            yq, yk = qk_rms_norm_pair(xs[0], xs[1], gains[0], gains[1])
+            torch.autograd.grad((yq, yk), (xs[0], xs[1], gains[0], gains[1]), dys)
     torch.cuda.synchronize()
 
 

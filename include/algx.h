@@ -87,6 +87,18 @@ int64_t algx_qknorm_bwd_workspace_bytes(int64_t rows, int32_t D, int32_t dtype);
 int32_t algx_qknorm_bwd(const void* x, const float* gain, const void* dy, void* dx, float* dgain,
                         void* workspace, int64_t rows, int32_t D, int32_t dtype, float eps,
                         void* stream);
+/* The same for the attention's q and k in one launch each way (the reference
+ * calls qk_rms_norm once per tensor, qk_norm.py:62-76): q and k have `rows`
+ * rows each and their own gains; the results equal two single-tensor calls
+ * bit for bit. */
+int32_t algx_qknorm_pair_fwd(const void* xq, const void* xk, const float* gain_q,
+                             const float* gain_k, void* yq, void* yk, int64_t rows, int32_t D,
+                             int32_t dtype, float eps, void* stream);
+int64_t algx_qknorm_pair_bwd_workspace_bytes(int64_t rows, int32_t D, int32_t dtype);
+int32_t algx_qknorm_pair_bwd(const void* xq, const void* xk, const float* gain_q,
+                             const float* gain_k, const void* dyq, const void* dyk, void* dxq,
+                             void* dxk, float* dgain_q, float* dgain_k, void* workspace,
+                             int64_t rows, int32_t D, int32_t dtype, float eps, void* stream);
 
 /* -------------------------------------------------------------- attention
  * Replaces flash_attention's device work (src/algebraic/kernels/flash.py:763-857):

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from _tol import assert_bf16, assert_f32, rel_l2, to_np
-from algebraic_amd.kernels import fused_head, qk_rms_norm
+from algebraic_amd.kernels import fused_head, qk_rms_norm, qk_rms_norm_pair
 from oracle import head as OH
 from oracle import qknorm as OQ
 
@@ -49,6 +49,44 @@ def test_qk_norm_output_and_vjp(dtype, eps, shape):
         tau = torch.rsqrt((xf * xf).mean(-1, keepdim=True) + eps)
         dg = (dy.to(DEV).double() * xf * tau).reshape(-1, 64).sum(0)
         assert rel_l2(tg.grad, dg) <= 1e-4
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(1, 2, 256, 64), (8, 16, 2048, 64)])
+def test_qk_norm_pair_equals_two_calls(dtype, shape):
+    """The paired launch returns what two qk_rms_norm calls return, bit for bit
+    (y, dx and dgain of q and k), and the q half matches the oracle."""
+    rng = np.random.default_rng(563)
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    xs = [torch.from_numpy((2 * rng.standard_normal(shape)).astype(np.float32)).to(tdt)
+          for _ in range(2)]
+    gs = [torch.from_numpy((1 + 0.01 * rng.standard_normal(64)).astype(np.float32))
+          for _ in range(2)]
+    dys = [torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(tdt)
+           for _ in range(2)]
+    ins = [[t.to(DEV).requires_grad_(True) for t in (x, g)] for x, g in zip(xs, gs)]
+    single = [qk_rms_norm(x, g, block=256) for x, g in ins]
+    torch.autograd.backward(single, [dy.to(DEV) for dy in dys])
+    ins2 = [[t.to(DEV).requires_grad_(True) for t in (x, g)] for x, g in zip(xs, gs)]
+    pair = qk_rms_norm_pair(ins2[0][0], ins2[1][0], ins2[0][1], ins2[1][1], block=256)
+    torch.autograd.backward(pair, [dy.to(DEV) for dy in dys])
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert torch.equal(pair[i], single[i]), f"y[{i}]"
+        assert torch.equal(ins2[i][0].grad, ins[i][0].grad), f"dx[{i}]"
+        assert torch.equal(ins2[i][1].grad, ins[i][1].grad), f"dgain[{i}]"
+    sl = (slice(0, 1), slice(0, 2))
+    want = OQ.forward(to_np(xs[0][sl]), to_np(gs[0]), 1e-5, dtype)
+    (assert_f32 if dtype == "f32" else assert_bf16)(pair[0][sl], want, what="y_q")
+
+
+def test_qk_norm_pair_validation():
+    q = torch.zeros((2, 4, 64), device=DEV)
+    g = torch.ones(64, device=DEV)
+    with pytest.raises(ValueError):
+        qk_rms_norm_pair(q, torch.zeros((2, 8, 64), device=DEV), g, g, block=8)
+    with pytest.raises(ValueError):
+        qk_rms_norm_pair(q, q.bfloat16(), g, g, block=8)
 
 
 def _head_inputs(N, d, V, seed, escale):
