@@ -211,10 +211,8 @@ extern "C" int32_t algx_attn_bwd(const void* q, const void* k, const void* v, co
                                   dsink, B, H, T, D, dtype, kl, kh, guard, s))
     return rc;
   if (mfma) {
-    const char* pp = std::getenv("ALGX_BWD_PP");
-    const bool use_pp = pp != nullptr && pp[0] == '1';
-    if (int32_t rc = (use_pp ? launch_bwd_pp : launch_bwd_mfma)(q, k, v, stat, di, dout, dq_acc,
-                                                                 dk, dv, B, H, T, kl, kh, guard, s))
+    if (int32_t rc = launch_bwd_mfma(q, k, v, stat, di, dout, dq_acc, dk, dv, B, H, T, kl, kh,
+                                     guard, s))
       return rc;
     return launch_dq_finish(dq_acc, dq, rows * D, dtype, kl, kh, guard, q_scale, s);
   }

@@ -54,10 +54,5 @@ int32_t launch_bwd_mfma(const void* q_s, const void* k, const void* v, const flo
                         const float* di, const void* dout, float* dq_acc, void* dk, void* dv,
                         int B, int H, int T, const KVariant& lo, const KVariant& hi,
                         const int32_t* guard, hipStream_t s);
-// The same product with the two-group ping-pong schedule.
-int32_t launch_bwd_pp(const void* q_s, const void* k, const void* v, const float* stat,
-                      const float* di, const void* dout, float* dq_acc, void* dk, void* dv,
-                      int B, int H, int T, const KVariant& lo, const KVariant& hi,
-                      const int32_t* guard, hipStream_t s);
 
 }  // namespace algx
