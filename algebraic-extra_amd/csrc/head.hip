@@ -216,6 +216,142 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   }
 }
 
+// ------------------------------------------------ direct-to-LDS GEMM core
+// The same product with the stages moved from memory straight into LDS by
+// LDS-DMA loads (global_load_lds_dwordx4: lane i of a wave's load writes its
+// 16 bytes at the destination + 16 i), so no registers stage them and no LDS
+// stores are issued; a ring of four stages keeps the loads three stages ahead
+// of the MFMAs with one barrier per stage. Stages are unpadded, with their
+// 16-byte chunks XOR-permuted so that the operand reads meet every LDS bank
+// once per pass: [mn][k] tiles (64-byte rows) keep chunk c of row r at
+// c ^ ((r >> 2) & 3), [k][mn] tiles (512-byte rows) at c ^ 4 (r & 3). Needs
+// K % BK == 0 (no partial stage); rows (or columns) past the operand's extent
+// load the operand's first bytes, which only reach outputs that are never
+// stored.
+constexpr int kDmaStages = 4;
+constexpr int kDmaOpElems = BM * BK;            // one operand stage: 8192 bf16
+
+// Source of this lane's 16 bytes in 1 KB block `blk` of a stage at k = 0.
+template <bool KC>
+__device__ __forceinline__ const bf16* dma_src(const Operand& op, int mn0, int blk, int lane) {
+  if (KC) {
+    const int r = 16 * blk + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+    const int row = mn0 + r;
+    return row < op.rows ? op.p + (int64_t)row * op.ld + 8 * c : op.p;
+  } else {
+    const int r = 2 * blk + (lane >> 5), c = (lane & 31) ^ (4 * (r & 3));
+    const int col = mn0 + 8 * c;
+    return col < op.rows ? op.p + (int64_t)r * op.ld + col : op.p;
+  }
+}
+
+// MFMA operand (as `operand`) from a swizzled DMA stage.
+template <bool KC>
+__device__ __forceinline__ bf16x8 operand_dma(const bf16* tile, int mn0, int k0, int lane) {
+  if (KC) {
+    const int r = mn0 + (lane & 31), c = (k0 >> 3) + (lane >> 5);
+    return *reinterpret_cast<const bf16x8*>(tile + r * BK + 8 * (c ^ ((r >> 2) & 3)));
+  } else {
+    const int G = lane >> 4, j = (lane >> 2) & 3, m = lane & 3;
+    const int r = k0 + 8 * (G >> 1) + j;
+    const int col = mn0 + 16 * (G & 1) + 4 * m;
+    const bf16* p = tile + r * BM + 8 * ((col >> 3) ^ (4 * (r & 3))) + (col & 7);
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * BM));
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+}
+
+// One LDS-DMA load of a wave: lane i's 16 bytes at src go to dst + 16 i (dst
+// wave-uniform). Issued as inline assembly so that the compiler does not
+// track it: its waitcnt pass cannot tell which LDS buffer such a load writes
+// and would wait for all of them before every LDS read; the ring below waits
+// for its own loads explicitly (wait_vm) before the barrier that publishes
+// them.
+__device__ __forceinline__ void dma16(const bf16* src, bf16* dst) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)dst);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
+               : "memory", "m0");
+}
+
+// s_waitcnt immediates: vmcnt(n) with expcnt and lgkmcnt unconstrained.
+template <int N> __device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+// Ring of four stage buffers (32 KB each: the A stage, then the B stage).
+struct DmaRing {
+  bf16* slot[kDmaStages];
+};
+
+template <bool AKC, bool BKC>
+__device__ __forceinline__ void gemm_tile_dma(const Operand& A, const Operand& B, int m0, int n0,
+                                              const DmaRing& ring, Acc& acc, int tid) {
+  const int w = tid >> 6, lane = tid & 63;
+  const int wm = w / NWN, wn = w % NWN;
+  const int nk = A.K / BK;
+  const bf16* sa0 = dma_src<AKC>(A, m0, 2 * w, lane);
+  const bf16* sa1 = dma_src<AKC>(A, m0, 2 * w + 1, lane);
+  const bf16* sb0 = dma_src<BKC>(B, n0, 2 * w, lane);
+  const bf16* sb1 = dma_src<BKC>(B, n0, 2 * w + 1, lane);
+  const int64_t stepA = AKC ? BK : (int64_t)BK * A.ld;
+  const int64_t stepB = BKC ? BK : (int64_t)BK * B.ld;
+  // The wave's two 1 KB blocks of each operand of stage kk -> slot S.
+  auto issue = [&](int kk, bf16* slot) {
+    bf16* dA = slot + 2 * w * 512;
+    bf16* dB = dA + kDmaOpElems;
+    const int64_t oa = kk * stepA, ob = kk * stepB;
+    dma16(sa0 + oa, dA);
+    dma16(sa1 + oa, dA + 512);
+    dma16(sb0 + ob, dB);
+    dma16(sb1 + ob, dB + 512);
+  };
+  auto mma = [&](const bf16* As) {
+    const bf16* Bs = As + kDmaOpElems;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8 a[TI], b[TJ];
+#pragma unroll
+      for (int i = 0; i < TI; ++i) a[i] = operand_dma<AKC>(As, WTM * wm + 32 * i, 16 * ks, lane);
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) b[j] = operand_dma<BKC>(Bs, WTN * wn + 32 * j, 16 * ks, lane);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc.v[i][j] = mfma32(a[i], b[j], acc.v[i][j]);
+    }
+  };
+  // Stage kk: wait until this wave's loads of it are complete (at most the
+  // loads of the up-to-two later stages outstanding), barrier (every wave's
+  // part visible; slot (kk + 3) % 4, read in iteration kk - 1, free), issue
+  // stage kk + 3, multiply. Slots are named statically: four stages a turn.
+  auto step = [&](int kk, bf16* cur, bf16* refill) {
+    const int later = nk - 1 - kk;
+    if (later >= 2)
+      wait_vm<8>();
+    else if (later == 1)
+      wait_vm<4>();
+    else
+      wait_vm<0>();
+    __syncthreads();
+    if (kk + kDmaStages - 1 < nk) issue(kk + kDmaStages - 1, refill);
+    mma(cur);
+  };
+  acc.zero();
+  wait_vm<0>();     // nothing older is counted with the ring's loads
+  __syncthreads();  // previous users of the ring are done
+  if (0 < nk) issue(0, ring.slot[0]);
+  if (1 < nk) issue(1, ring.slot[1]);
+  if (2 < nk) issue(2, ring.slot[2]);
+  for (int kk = 0; kk < nk; kk += 4) {
+    step(kk, ring.slot[0], ring.slot[3]);
+    if (kk + 1 < nk) step(kk + 1, ring.slot[1], ring.slot[0]);
+    if (kk + 2 < nk) step(kk + 2, ring.slot[2], ring.slot[1]);
+    if (kk + 3 < nk) step(kk + 3, ring.slot[3], ring.slot[2]);
+  }
+}
+
 // x^n, n = 2^log2n: unrolled squarings for a compile-time L2N > 0 (a runtime
 // loop inside the per-logit epilogue would cost a branch per logit).
 template <int L2N> __device__ __forceinline__ float pow_n(float x, int log2n) {
@@ -454,14 +590,17 @@ struct GemmJob {
   int tiles_n;  // output tiles along n
 };
 
-template <bool AKC, bool BKC, typename TOut, bool ACCUM>
-__device__ __forceinline__ void gemm_job(const GemmJob& jb, int tile, bf16* As, bf16* Bs,
-                                         int tid) {
+template <bool AKC, bool BKC, typename TOut, bool ACCUM, bool DMA>
+__device__ __forceinline__ void gemm_job(const GemmJob& jb, int tile, bf16* lds,
+                                         const DmaRing& ring, int tid) {
   const int w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
   const int wm = w / NWN, wn = w % NWN;
   const int m0 = (tile / jb.tiles_n) * BM, n0 = (tile % jb.tiles_n) * BN;
   Acc acc;
-  gemm_tile<AKC, BKC>(jb.A, jb.B, m0, n0, As, Bs, acc, tid);
+  if (DMA)
+    gemm_tile_dma<AKC, BKC>(jb.A, jb.B, m0, n0, ring, acc, tid);
+  else
+    gemm_tile<AKC, BKC>(jb.A, jb.B, m0, n0, lds, lds + 2 * kStageElems, acc, tid);
   TOut* C = reinterpret_cast<TOut*>(jb.C);
 #pragma unroll
   for (int i = 0; i < TI; ++i)
@@ -499,17 +638,25 @@ __device__ __forceinline__ int xcd_tile(int b, int ntiles, int tiles_n) {
 // tiles first): dh[t][c] = sum_v dz[t][v] E[v][c] in the first dh_slots
 // workgroups (n_dh tiles; dh_slots is n_dh rounded up to a multiple of 8),
 // then dE[v][c] (+)= sum_t dz[t][v] h[t][c].
-template <bool ACCUM>
+template <bool ACCUM, bool DMA>
 __global__ __launch_bounds__(kThreads) void head_grad_kernel(GemmJob dh, GemmJob de, int n_dh,
                                                              int dh_slots, int n_de) {
-  __shared__ __attribute__((aligned(16))) bf16 As[2 * kStageElems];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * kStageElems];
+  // DMA: four stage buffers of 2 x 16 KB; otherwise the two double-buffered
+  // operand stages of gemm_tile in the first of them.
+  constexpr int kSlot = DMA ? 2 * kDmaOpElems : 4 * kStageElems;
+  __shared__ __attribute__((aligned(16))) bf16 s0[kSlot];
+  __shared__ __attribute__((aligned(16))) bf16 s1[DMA ? 2 * kDmaOpElems : 8];
+  __shared__ __attribute__((aligned(16))) bf16 s2[DMA ? 2 * kDmaOpElems : 8];
+  __shared__ __attribute__((aligned(16))) bf16 s3[DMA ? 2 * kDmaOpElems : 8];
+  const DmaRing ring{{s0, s1, s2, s3}};
   const int b = blockIdx.x;
   if (b < dh_slots) {
-    if (b < n_dh) gemm_job<true, false, bf16, false>(dh, xcd_tile(b, n_dh, dh.tiles_n), As, Bs, threadIdx.x);
+    if (b < n_dh)
+      gemm_job<true, false, bf16, false, DMA>(dh, xcd_tile(b, n_dh, dh.tiles_n), s0, ring,
+                                              threadIdx.x);
   } else {
-    gemm_job<false, false, float, ACCUM>(de, xcd_tile(b - dh_slots, n_de, de.tiles_n), As, Bs,
-                                         threadIdx.x);
+    gemm_job<false, false, float, ACCUM, DMA>(de, xcd_tile(b - dh_slots, n_de, de.tiles_n), s0,
+                                              ring, threadIdx.x);
   }
 }
 
@@ -662,8 +809,13 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
     const int n_dh = ((ntok + BM - 1) / BM) * tn;
     const int n_de = ((V + BM - 1) / BM) * tn;
     const int dh_slots = (n_dh + 7) / 8 * 8;
-    launch_k(probe_for(ALGX_PROBE_HEAD_DE), tok0 == 0 ? head_grad_kernel<false> : head_grad_kernel<true>,
-             dim3(dh_slots + n_de), dim3(kThreads), s, jdh, jde, n_dh, dh_slots, n_de);
+    // LDS-DMA stages when both products have whole k stages (V and the
+    // chunk's token count multiples of BK).
+    const bool dma = V % BK == 0 && ntok % BK == 0;
+    auto gk = dma ? (tok0 == 0 ? head_grad_kernel<false, true> : head_grad_kernel<true, true>)
+                  : (tok0 == 0 ? head_grad_kernel<false, false> : head_grad_kernel<true, false>);
+    launch_k(probe_for(ALGX_PROBE_HEAD_DE), gk, dim3(dh_slots + n_de), dim3(kThreads), s, jdh, jde,
+             n_dh, dh_slots, n_de);
     if (int32_t rc = check_launch("head_grad")) return rc;
   }
   return 0;
