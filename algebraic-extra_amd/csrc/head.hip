@@ -220,8 +220,8 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 // The same product with the stages moved from memory straight into LDS by
 // LDS-DMA loads (global_load_lds_dwordx4: lane i of a wave's load writes its
 // 16 bytes at the destination + 16 i), so no registers stage them and no LDS
-// stores are issued; a ring of four stages keeps the loads three stages ahead
-// of the MFMAs with one barrier per stage. Stages are unpadded, with their
+// stores are issued; a ring of four stages keeps the loads two stages ahead
+// of the operand reads, with one barrier per stage. Stages are unpadded, with their
 // 16-byte chunks XOR-permuted so that the operand reads meet every LDS bank
 // once per pass: [mn][k] tiles (64-byte rows) keep chunk c of row r at
 // c ^ ((r >> 2) & 3), [k][mn] tiles (512-byte rows) at c ^ 4 (r & 3). Needs
@@ -268,9 +268,7 @@ __device__ __forceinline__ bf16x8 operand_dma(const bf16* tile, int mn0, int k0,
 // and would wait for all of them before every LDS read; the ring below waits
 // for its own loads explicitly (wait_vm) before the barrier that publishes
 // them.
-__device__ __forceinline__ void dma16(const bf16* src, bf16* dst) {
-  const unsigned lds = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)dst);
+__device__ __forceinline__ void dma16(const bf16* src, unsigned lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
                : "memory", "m0");
 }
@@ -280,14 +278,20 @@ template <int N> __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
 
-// Ring of four stage buffers (32 KB each: the A stage, then the B stage).
+// Ring of stage buffers (32 KB each: the A stage, then the B stage).
 struct DmaRing {
   bf16* slot[kDmaStages];
 };
 
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 template <bool AKC, bool BKC>
 __device__ __forceinline__ void gemm_tile_dma(const Operand& A, const Operand& B, int m0, int n0,
                                               const DmaRing& ring, Acc& acc, int tid) {
+  constexpr int S = kDmaStages, L = S - 2;  // stages in flight beyond the one being read
   const int w = tid >> 6, lane = tid & 63;
   const int wm = w / NWN, wn = w % NWN;
   const int nk = A.K / BK;
@@ -297,59 +301,107 @@ __device__ __forceinline__ void gemm_tile_dma(const Operand& A, const Operand& B
   const bf16* sb1 = dma_src<BKC>(B, n0, 2 * w + 1, lane);
   const int64_t stepA = AKC ? BK : (int64_t)BK * A.ld;
   const int64_t stepB = BKC ? BK : (int64_t)BK * B.ld;
-  // The wave's two 1 KB blocks of each operand of stage kk -> slot S.
+  // Byte offset of the wave's two 1 KB blocks in an operand stage (uniform).
+  const unsigned wofs = 2048u * __builtin_amdgcn_readfirstlane(w);
+  // The wave's two 1 KB blocks of each operand of stage kk -> slot.
   auto issue = [&](int kk, bf16* slot) {
-    bf16* dA = slot + 2 * w * 512;
-    bf16* dB = dA + kDmaOpElems;
-    const int64_t oa = kk * stepA, ob = kk * stepB;
+    const unsigned dA = lds_addr(slot) + wofs, dB = dA + 2 * kDmaOpElems;
+    // Stage offsets as scalars computed here (the compiler would otherwise
+    // keep one vector induction variable per unrolled stage).
+    int64_t oa = kk * stepA, ob = kk * stepB;
+    asm volatile("" : "+s"(oa), "+s"(ob));
     dma16(sa0 + oa, dA);
-    dma16(sa1 + oa, dA + 512);
+    dma16(sa1 + oa, dA + 1024);
     dma16(sb0 + ob, dB);
-    dma16(sb1 + ob, dB + 512);
+    dma16(sb1 + ob, dB + 1024);
   };
-  auto mma = [&](const bf16* As) {
-    const bf16* Bs = As + kDmaOpElems;
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 a[TI], b[TJ];
-#pragma unroll
-      for (int i = 0; i < TI; ++i) a[i] = operand_dma<AKC>(As, WTM * wm + 32 * i, 16 * ks, lane);
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) b[j] = operand_dma<BKC>(Bs, WTN * wn + 32 * j, 16 * ks, lane);
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) acc.v[i][j] = mfma32(a[i], b[j], acc.v[i][j]);
-    }
-  };
-  // Stage kk: wait until this wave's loads of it are complete (at most the
-  // loads of the up-to-two later stages outstanding), barrier (every wave's
-  // part visible; slot (kk + 3) % 4, read in iteration kk - 1, free), issue
-  // stage kk + 3, multiply. Slots are named statically: four stages a turn.
-  auto step = [&](int kk, bf16* cur, bf16* refill) {
-    const int later = nk - 1 - kk;
-    if (later >= 2)
-      wait_vm<8>();
+  // Wait until at most `later` of this wave's stages are still loading (four
+  // loads a stage; the loads complete in issue order).
+  auto wait_stages = [](int later) {
+    static_assert(L <= 4, "the vmcnt immediates below cover up to three later stages");
+    if (later <= 0)
+      wait_vm<0>();
     else if (later == 1)
       wait_vm<4>();
+    else if (later == 2)
+      wait_vm<8>();
     else
-      wait_vm<0>();
-    __syncthreads();
-    if (kk + kDmaStages - 1 < nk) issue(kk + kDmaStages - 1, refill);
-    mma(cur);
+      wait_vm<12>();
+  };
+  // Operands of one 16-wide k step (ks) of a stage into registers.
+  auto rd = [&](const bf16* As, int ks, bf16x8 (&a)[TI], bf16x8 (&b)[TJ]) {
+    const bf16* Bs = As + kDmaOpElems;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) b[j] = operand_dma<BKC>(Bs, WTN * wn + 32 * j, 16 * ks, lane);
+#pragma unroll
+    for (int i = 0; i < TI; ++i) a[i] = operand_dma<AKC>(As, WTM * wm + 32 * i, 16 * ks, lane);
+  };
+  auto mm = [&](const bf16x8 (&a)[TI], const bf16x8 (&b)[TJ]) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) acc.v[i][j] = mfma32(a[i], b[j], acc.v[i][j]);
   };
   acc.zero();
   wait_vm<0>();     // nothing older is counted with the ring's loads
   __syncthreads();  // previous users of the ring are done
-  if (0 < nk) issue(0, ring.slot[0]);
-  if (1 < nk) issue(1, ring.slot[1]);
-  if (2 < nk) issue(2, ring.slot[2]);
-  for (int kk = 0; kk < nk; kk += 4) {
-    step(kk, ring.slot[0], ring.slot[3]);
-    if (kk + 1 < nk) step(kk + 1, ring.slot[1], ring.slot[0]);
-    if (kk + 2 < nk) step(kk + 2, ring.slot[2], ring.slot[1]);
-    if (kk + 3 < nk) step(kk + 3, ring.slot[3], ring.slot[2]);
+  // Stages 0 .. S-2 now, then stage kk + S - 1 at the barrier of stage kk
+  // (into the slot of stage kk - 1), so every stage is issued two stages
+  // before its operands are read.
+#pragma unroll
+  for (int u = 0; u < S - 1; ++u)
+    if (u < nk) issue(u, ring.slot[u]);
+  wait_stages(min(S - 2, nk - 1));
+  __syncthreads();
+  // Register double buffer over half stages: the operands of the next half
+  // stage are read while the MFMAs of the current one run. The barrier sits
+  // between a stage's halves: it publishes stage kk + 1 (whose first half is
+  // read next). It does not wait for this wave's LDS reads: those in flight
+  // read slot kk % S, which no load refills before the next barrier. On the
+  // last stage the reads of "stage nk" fetch a stale slot and are unused.
+  bf16x8 xa[TI], xb[TJ], ya[TI], yb[TJ];
+  rd(ring.slot[0], 0, xa, xb);
+  auto step = [&](int kk, const bf16* cur, const bf16* nxt, bf16* refill) {
+    rd(cur, 1, ya, yb);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(xa, xb);
+    __builtin_amdgcn_sched_barrier(0);
+    // Wait for stage kk + 1; the stages issued after it may stay in flight.
+    wait_stages(min(kk + S - 2, nk - 1) - (kk + 1));
+    asm volatile("s_barrier" ::: "memory");
+    if (kk + S - 1 < nk) issue(kk + S - 1, refill);
+    rd(nxt, 0, xa, xb);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(ya, yb);
+  };
+  // Slots are named statically: S stages a turn.
+  for (int kk = 0; kk < nk; kk += S) {
+#pragma unroll
+    for (int u = 0; u < S; ++u)
+      if (kk + u < nk)
+        step(kk + u, ring.slot[u], ring.slot[(u + 1) % S], ring.slot[(u + S - 1) % S]);
   }
+}
+
+// LDS of a kernel built on the GEMM cores (DMA: a compile-time bool in
+// scope): four 32 KB stage buffers of the direct-to-LDS ring, or the two
+// double-buffered operand stages of gemm_tile in the first of them.
+#define GEMM_LDS_STAGES                                                                  \
+  __shared__ __attribute__((aligned(16))) bf16 s0[DMA ? 2 * kDmaOpElems : 4 * kStageElems]; \
+  __shared__ __attribute__((aligned(16))) bf16 s1[DMA ? 2 * kDmaOpElems : 8];               \
+  __shared__ __attribute__((aligned(16))) bf16 s2[DMA ? 2 * kDmaOpElems : 8];               \
+  __shared__ __attribute__((aligned(16))) bf16 s3[DMA ? 2 * kDmaOpElems : 8];               \
+  const DmaRing ring{{s0, s1, s2, s3}}
+
+// Product of one output tile with both operands k-contiguous, on the
+// direct-to-LDS ring (DMA: K a multiple of BK) or on gemm_tile.
+template <bool DMA>
+__device__ __forceinline__ void gemm_any(const Operand& A, const Operand& B, int m0, int n0,
+                                         bf16* lds, const DmaRing& ring, Acc& acc, int tid) {
+  if constexpr (DMA)
+    gemm_tile_dma<true, true>(A, B, m0, n0, ring, acc, tid);
+  else
+    gemm_tile<true, true>(A, B, m0, n0, lds, lds + 2 * kStageElems, acc, tid);
 }
 
 // x^n, n = 2^log2n: unrolled squarings for a compile-time L2N > 0 (a runtime
@@ -373,13 +425,12 @@ __device__ __forceinline__ float alg_weight(float z, float inv_c, float clamp, i
 
 // Forward statistics. grid = (token blocks) x (vocabulary chunks).
 // partial[(chunk * N + token) * 2 + {0,1}] = (m, l) for ce, (-, l) for alg_ce.
-template <int KIND, int L2N>
+template <int KIND, int L2N, bool DMA>
 __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
     const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
     float* __restrict__ zt, float* __restrict__ partial, int N, int d, int V, int log2n,
     float inv_c, float clamp) {
-  __shared__ __attribute__((aligned(16))) bf16 As[2 * kStageElems];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * kStageElems];
+  GEMM_LDS_STAGES;
   __shared__ float red_m[2][BN], red_l[2][BN];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
   const int wm = w / NWN, wn = w % NWN;
@@ -454,7 +505,7 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
   Acc acc;
   for (int t = t_begin; t < t_end; ++t) {
     const int m0 = t * BM;
-    gemm_tile<true, true>(A, B, m0, n0, As, Bs, acc, tid);
+    gemm_any<DMA>(A, B, m0, n0, s0, ring, acc, tid);
     if (m0 + BM <= V)
       consume(std::true_type{}, m0, acc);
     else
@@ -523,13 +574,12 @@ __global__ __launch_bounds__(256) void head_stat_kernel(const float* __restrict_
 }
 
 // dz tile of a token chunk: dz[t][v] = bf16(f(z) * scale), 0 for padded v.
-template <int KIND, int L2N>
+template <int KIND, int L2N, bool DMA>
 __global__ __launch_bounds__(kThreads) void head_dz_kernel(
     const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
     const float* __restrict__ stat, const float* __restrict__ scale, bf16* __restrict__ dz,
     int64_t ldz, int tok0, int ntok, int d, int V, int log2n, float inv_c, float clamp) {
-  __shared__ __attribute__((aligned(16))) bf16 As[2 * kStageElems];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[2 * kStageElems];
+  GEMM_LDS_STAGES;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
   const int wm = w / NWN, wn = w % NWN;
   const int n0 = blockIdx.x * BN;   // token offset inside the chunk
@@ -537,7 +587,7 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
   const Operand A{e, d, V, d};
   const Operand B{h + (int64_t)tok0 * d, d, ntok, d};
   Acc acc;
-  gemm_tile<true, true>(A, B, m0, n0, As, Bs, acc, tid);
+  gemm_any<DMA>(A, B, m0, n0, s0, ring, acc, tid);
   const float sc = scale[0];
   // FULL: every row of the tile is inside the vocabulary (all but the last
   // vocabulary tile), so no row mask is formed.
@@ -641,14 +691,7 @@ __device__ __forceinline__ int xcd_tile(int b, int ntiles, int tiles_n) {
 template <bool ACCUM, bool DMA>
 __global__ __launch_bounds__(kThreads) void head_grad_kernel(GemmJob dh, GemmJob de, int n_dh,
                                                              int dh_slots, int n_de) {
-  // DMA: four stage buffers of 2 x 16 KB; otherwise the two double-buffered
-  // operand stages of gemm_tile in the first of them.
-  constexpr int kSlot = DMA ? 2 * kDmaOpElems : 4 * kStageElems;
-  __shared__ __attribute__((aligned(16))) bf16 s0[kSlot];
-  __shared__ __attribute__((aligned(16))) bf16 s1[DMA ? 2 * kDmaOpElems : 8];
-  __shared__ __attribute__((aligned(16))) bf16 s2[DMA ? 2 * kDmaOpElems : 8];
-  __shared__ __attribute__((aligned(16))) bf16 s3[DMA ? 2 * kDmaOpElems : 8];
-  const DmaRing ring{{s0, s1, s2, s3}};
+  GEMM_LDS_STAGES;
   const int b = blockIdx.x;
   if (b < dh_slots) {
     if (b < n_dh)
@@ -694,24 +737,31 @@ typedef void (*HeadFwdFn)(const bf16*, const bf16*, const int32_t*, float*, floa
 typedef void (*HeadDzFn)(const bf16*, const bf16*, const int32_t*, const float*, const float*,
                          bf16*, int64_t, int, int, int, int, int, float, float);
 
-// Kernel instance for (kind, n): alg_ce with n = 8, 16 or 32 gets unrolled powers.
-HeadFwdFn pick_head_fwd(int kind, int log2n) {
-  if (kind == ALGX_HEAD_CE) return head_fwd_kernel<ALGX_HEAD_CE, 0>;
+// Kernel instance for (kind, n): alg_ce with n = 8, 16 or 32 gets unrolled
+// powers. DMA (the direct-to-LDS ring) when d is a multiple of BK.
+template <bool DMA> HeadFwdFn pick_head_fwd_as(int kind, int log2n) {
+  if (kind == ALGX_HEAD_CE) return head_fwd_kernel<ALGX_HEAD_CE, 0, DMA>;
   switch (log2n) {
-    case 3: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 3>;
-    case 4: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 4>;
-    case 5: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 5>;
-    default: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 0>;
+    case 3: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 3, DMA>;
+    case 4: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 4, DMA>;
+    case 5: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 5, DMA>;
+    default: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 0, DMA>;
   }
 }
-HeadDzFn pick_head_dz(int kind, int log2n) {
-  if (kind == ALGX_HEAD_CE) return head_dz_kernel<ALGX_HEAD_CE, 0>;
+template <bool DMA> HeadDzFn pick_head_dz_as(int kind, int log2n) {
+  if (kind == ALGX_HEAD_CE) return head_dz_kernel<ALGX_HEAD_CE, 0, DMA>;
   switch (log2n) {
-    case 3: return head_dz_kernel<ALGX_HEAD_ALG_CE, 3>;
-    case 4: return head_dz_kernel<ALGX_HEAD_ALG_CE, 4>;
-    case 5: return head_dz_kernel<ALGX_HEAD_ALG_CE, 5>;
-    default: return head_dz_kernel<ALGX_HEAD_ALG_CE, 0>;
+    case 3: return head_dz_kernel<ALGX_HEAD_ALG_CE, 3, DMA>;
+    case 4: return head_dz_kernel<ALGX_HEAD_ALG_CE, 4, DMA>;
+    case 5: return head_dz_kernel<ALGX_HEAD_ALG_CE, 5, DMA>;
+    default: return head_dz_kernel<ALGX_HEAD_ALG_CE, 0, DMA>;
   }
+}
+HeadFwdFn pick_head_fwd(int kind, int log2n, int d) {
+  return d % BK == 0 ? pick_head_fwd_as<true>(kind, log2n) : pick_head_fwd_as<false>(kind, log2n);
+}
+HeadDzFn pick_head_dz(int kind, int log2n, int d) {
+  return d % BK == 0 ? pick_head_dz_as<true>(kind, log2n) : pick_head_dz_as<false>(kind, log2n);
 }
 
 int nchunks_of(int V) {
@@ -751,7 +801,7 @@ extern "C" int32_t algx_head_fwd(const void* h, const void* E, const int32_t* ta
                         kind, log2n, inv_c, clamp, s);
   {
     const Probe probe = probe_for(ALGX_PROBE_HEAD_FWD);
-    launch_k(probe, pick_head_fwd(kind, log2n),
+    launch_k(probe, pick_head_fwd(kind, log2n, d),
              grid, dim3(kThreads), s, (const bf16*)h, (const bf16*)E, targets, zt, partial, N, d,
              V, log2n, inv_c, clamp);
   }
@@ -795,7 +845,7 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
     const int ntok = min(csize, N - tok0);
     dim3 gdz((ntok + BN - 1) / BN, (V + BM - 1) / BM);
     launch_k(probe_for(ALGX_PROBE_HEAD_DZ),
-             pick_head_dz(kind, log2n),
+             pick_head_dz(kind, log2n, d),
              gdz, dim3(kThreads), s, hb, eb, targets, stat, scale, dz, ldz, tok0, ntok, d, V, log2n,
              inv_c, clamp);
     if (int32_t rc = check_launch("head_dz")) return rc;
