@@ -34,7 +34,7 @@ constexpr int kChunks = BM * BK / 8 / kThreads;  // 16-byte chunks per thread pe
 static_assert(BM == BN && (BM / 8) * (kThreads / (BM / 8)) == kThreads &&
                   kChunks * (kThreads / (BM / 8)) == BK,
               "[k][mn] loader: BM/8 threads per k row group, kChunks k rows each");
-constexpr int kVocabChunkTiles = 8;  // vocabulary tiles per forward workgroup
+constexpr int kFwdWorkgroups = 256;  // forward grid target: one workgroup per CU
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -288,14 +288,21 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
   return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-template <bool AKC, bool BKC>
-__device__ __forceinline__ void gemm_tile_dma(const Operand& A, const Operand& B, int m0, int n0,
-                                              const DmaRing& ring, Acc& acc, int tid) {
+// Products of `ntiles` output tiles that share the B rows n0: tile t uses A
+// rows m0 + t BM; epi(t, m0 + t BM, acc) receives each finished tile. The
+// ring streams across the tiles, so a tile's first stages load during the
+// previous tile's last stages and epilogue. Several tiles need the tile's
+// stage count to be a multiple of the ring's (every tile starts at slot 0).
+template <bool AKC, bool BKC, typename Epi>
+__device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B, int m0,
+                                             int ntiles, int n0, const DmaRing& ring, Acc& acc,
+                                             int tid, Epi&& epi) {
   constexpr int S = kDmaStages, L = S - 2;  // stages in flight beyond the one being read
   const int w = tid >> 6, lane = tid & 63;
   const int wm = w / NWN, wn = w % NWN;
   const int nk = A.K / BK;
-  const bf16* sa0 = dma_src<AKC>(A, m0, 2 * w, lane);
+  const int G = ntiles * nk;  // stages of the whole sequence
+  const bf16* sa0 = dma_src<AKC>(A, m0, 2 * w, lane);  // A sources of the tile being issued
   const bf16* sa1 = dma_src<AKC>(A, m0, 2 * w + 1, lane);
   const bf16* sb0 = dma_src<BKC>(B, n0, 2 * w, lane);
   const bf16* sb1 = dma_src<BKC>(B, n0, 2 * w + 1, lane);
@@ -303,20 +310,22 @@ __device__ __forceinline__ void gemm_tile_dma(const Operand& A, const Operand& B
   const int64_t stepB = BKC ? BK : (int64_t)BK * B.ld;
   // Byte offset of the wave's two 1 KB blocks in an operand stage (uniform).
   const unsigned wofs = 2048u * __builtin_amdgcn_readfirstlane(w);
-  // The wave's two 1 KB blocks of each operand of stage kk -> slot.
-  auto issue = [&](int kk, bf16* slot) {
+  // The wave's two 1 KB blocks of each operand of stage kk (A sources a0/a1)
+  // -> slot.
+  auto issue = [&](const bf16* a0, const bf16* a1, int kk, bf16* slot) {
     const unsigned dA = lds_addr(slot) + wofs, dB = dA + 2 * kDmaOpElems;
     // Stage offsets as scalars computed here (the compiler would otherwise
     // keep one vector induction variable per unrolled stage).
     int64_t oa = kk * stepA, ob = kk * stepB;
     asm volatile("" : "+s"(oa), "+s"(ob));
-    dma16(sa0 + oa, dA);
-    dma16(sa1 + oa, dA + 1024);
+    dma16(a0 + oa, dA);
+    dma16(a1 + oa, dA + 1024);
     dma16(sb0 + ob, dB);
     dma16(sb1 + ob, dB + 1024);
   };
   // Wait until at most `later` of this wave's stages are still loading (four
-  // loads a stage; the loads complete in issue order).
+  // loads a stage; the loads complete in issue order, and any later vector
+  // memory operation only makes the wait stricter).
   auto wait_stages = [](int later) {
     static_assert(L <= 4, "the vmcnt immediates below cover up to three later stages");
     if (later <= 0)
@@ -345,42 +354,69 @@ __device__ __forceinline__ void gemm_tile_dma(const Operand& A, const Operand& B
   acc.zero();
   wait_vm<0>();     // nothing older is counted with the ring's loads
   __syncthreads();  // previous users of the ring are done
-  // Stages 0 .. S-2 now, then stage kk + S - 1 at the barrier of stage kk
-  // (into the slot of stage kk - 1), so every stage is issued two stages
-  // before its operands are read.
+  // Stages 0 .. S-2 now (all of the first tile when there are several), then
+  // stage g + S - 1 at the barrier of stage g (into the slot of stage g - 1),
+  // so every stage is issued two stages before its operands are read.
 #pragma unroll
   for (int u = 0; u < S - 1; ++u)
-    if (u < nk) issue(u, ring.slot[u]);
-  wait_stages(min(S - 2, nk - 1));
+    if (u < nk) issue(sa0, sa1, u, ring.slot[u]);
+  wait_stages(min(S - 2, G - 1));
   __syncthreads();
   // Register double buffer over half stages: the operands of the next half
   // stage are read while the MFMAs of the current one run. The barrier sits
-  // between a stage's halves: it publishes stage kk + 1 (whose first half is
+  // between a stage's halves: it publishes stage g + 1 (whose first half is
   // read next). It does not wait for this wave's LDS reads: those in flight
-  // read slot kk % S, which no load refills before the next barrier. On the
-  // last stage the reads of "stage nk" fetch a stale slot and are unused.
+  // read the slot of stage g, which no load refills before the next barrier.
+  // On the last stage the reads of "stage G" fetch a stale slot and are unused.
   bf16x8 xa[TI], xb[TJ], ya[TI], yb[TJ];
   rd(ring.slot[0], 0, xa, xb);
-  auto step = [&](int kk, const bf16* cur, const bf16* nxt, bf16* refill) {
-    rd(cur, 1, ya, yb);
-    __builtin_amdgcn_sched_barrier(0);
-    mm(xa, xb);
-    __builtin_amdgcn_sched_barrier(0);
-    // Wait for stage kk + 1; the stages issued after it may stay in flight.
-    wait_stages(min(kk + S - 2, nk - 1) - (kk + 1));
-    asm volatile("s_barrier" ::: "memory");
-    if (kk + S - 1 < nk) issue(kk + S - 1, refill);
-    rd(nxt, 0, xa, xb);
-    __builtin_amdgcn_sched_barrier(0);
-    mm(ya, yb);
-  };
-  // Slots are named statically: S stages a turn.
-  for (int kk = 0; kk < nk; kk += S) {
+  for (int t = 0; t < ntiles; ++t) {
+    // A sources of the next tile, for the stages issued near this tile's end.
+    const bf16* na0 = sa0;
+    const bf16* na1 = sa1;
+    if (t + 1 < ntiles) {
+      na0 = dma_src<AKC>(A, m0 + (t + 1) * BM, 2 * w, lane);
+      na1 = dma_src<AKC>(A, m0 + (t + 1) * BM, 2 * w + 1, lane);
+    }
+    const int g0 = t * nk;
+    auto step = [&](int kk, const bf16* cur, const bf16* nxt, bf16* refill) {
+      rd(cur, 1, ya, yb);
+      __builtin_amdgcn_sched_barrier(0);
+      mm(xa, xb);
+      __builtin_amdgcn_sched_barrier(0);
+      // Wait for stage g + 1; the stages issued after it may stay in flight.
+      const int g = g0 + kk;
+      wait_stages(min(g + S - 2, G - 1) - (g + 1));
+      asm volatile("s_barrier" ::: "memory");
+      if (kk + S - 1 < nk)
+        issue(sa0, sa1, kk + S - 1, refill);
+      else if (t + 1 < ntiles)
+        issue(na0, na1, kk + S - 1 - nk, refill);
+      rd(nxt, 0, xa, xb);
+      __builtin_amdgcn_sched_barrier(0);
+      mm(ya, yb);
+    };
+    // Slots are named statically: S stages a turn.
+    for (int kk = 0; kk < nk; kk += S) {
 #pragma unroll
-    for (int u = 0; u < S; ++u)
-      if (kk + u < nk)
-        step(kk + u, ring.slot[u], ring.slot[(u + 1) % S], ring.slot[(u + S - 1) % S]);
+      for (int u = 0; u < S; ++u)
+        if (kk + u < nk)
+          step(kk + u, ring.slot[u], ring.slot[(u + 1) % S], ring.slot[(u + S - 1) % S]);
+    }
+    epi(t, m0 + t * BM, acc);
+    acc.zero();
+    sa0 = na0;
+    sa1 = na1;
   }
+}
+
+// Full-K product of one output tile on the direct-to-LDS ring.
+template <bool AKC, bool BKC>
+__device__ __forceinline__ void gemm_tile_dma(const Operand& A, const Operand& B, int m0, int n0,
+                                              const DmaRing& ring, Acc& acc, int tid) {
+  Acc out;
+  gemm_seq_dma<AKC, BKC>(A, B, m0, 1, n0, ring, out, tid,
+                         [&](int, int, Acc& a) { acc = a; });
 }
 
 // LDS of a kernel built on the GEMM cores (DMA: a compile-time bool in
@@ -392,17 +428,6 @@ __device__ __forceinline__ void gemm_tile_dma(const Operand& A, const Operand& B
   __shared__ __attribute__((aligned(16))) bf16 s2[DMA ? 2 * kDmaOpElems : 8];               \
   __shared__ __attribute__((aligned(16))) bf16 s3[DMA ? 2 * kDmaOpElems : 8];               \
   const DmaRing ring{{s0, s1, s2, s3}}
-
-// Product of one output tile with both operands k-contiguous, on the
-// direct-to-LDS ring (DMA: K a multiple of BK) or on gemm_tile.
-template <bool DMA>
-__device__ __forceinline__ void gemm_any(const Operand& A, const Operand& B, int m0, int n0,
-                                         bf16* lds, const DmaRing& ring, Acc& acc, int tid) {
-  if constexpr (DMA)
-    gemm_tile_dma<true, true>(A, B, m0, n0, ring, acc, tid);
-  else
-    gemm_tile<true, true>(A, B, m0, n0, lds, lds + 2 * kStageElems, acc, tid);
-}
 
 // x^n, n = 2^log2n: unrolled squarings for a compile-time L2N > 0 (a runtime
 // loop inside the per-logit epilogue would cost a branch per logit).
@@ -423,13 +448,16 @@ __device__ __forceinline__ float alg_weight(float z, float inv_c, float clamp, i
   return pow_n<L2N>(rho_fast(x, r), log2n);
 }
 
-// Forward statistics. grid = (token blocks) x (vocabulary chunks).
+// Forward statistics. grid = (token blocks) x (vocabulary chunks of
+// chunk_tiles tiles).
 // partial[(chunk * N + token) * 2 + {0,1}] = (m, l) for ce, (-, l) for alg_ce.
+// DMA: the direct-to-LDS ring streamed over the chunk's tiles (d a multiple
+// of BK * kDmaStages).
 template <int KIND, int L2N, bool DMA>
 __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
     const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
     float* __restrict__ zt, float* __restrict__ partial, int N, int d, int V, int log2n,
-    float inv_c, float clamp) {
+    float inv_c, float clamp, int chunk_tiles) {
   GEMM_LDS_STAGES;
   __shared__ float red_m[2][BN], red_l[2][BN];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
@@ -437,8 +465,8 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
   const int n0 = blockIdx.x * BN;
   const int chunk = blockIdx.y;
   const int ntiles_v = (V + BM - 1) / BM;
-  const int t_begin = chunk * kVocabChunkTiles;
-  const int t_end = min(ntiles_v, t_begin + kVocabChunkTiles);
+  const int t_begin = chunk * chunk_tiles;
+  const int t_end = min(ntiles_v, t_begin + chunk_tiles);
   const Operand A{e, d, V, d};
   const Operand B{h, d, N, d};
   int tok[TJ], tgt[TJ];
@@ -503,13 +531,23 @@ __global__ __launch_bounds__(kThreads) void head_fwd_kernel(
     }
   };
   Acc acc;
-  for (int t = t_begin; t < t_end; ++t) {
-    const int m0 = t * BM;
-    gemm_any<DMA>(A, B, m0, n0, s0, ring, acc, tid);
-    if (m0 + BM <= V)
-      consume(std::true_type{}, m0, acc);
-    else
-      consume(std::false_type{}, m0, acc);
+  if constexpr (DMA) {
+    gemm_seq_dma<true, true>(A, B, t_begin * BM, t_end - t_begin, n0, ring, acc, tid,
+                             [&](int, int m0, const Acc& a) {
+                               if (m0 + BM <= V)
+                                 consume(std::true_type{}, m0, a);
+                               else
+                                 consume(std::false_type{}, m0, a);
+                             });
+  } else {
+    for (int t = t_begin; t < t_end; ++t) {
+      const int m0 = t * BM;
+      gemm_tile<true, true>(A, B, m0, n0, s0, s0 + 2 * kStageElems, acc, tid);
+      if (m0 + BM <= V)
+        consume(std::true_type{}, m0, acc);
+      else
+        consume(std::false_type{}, m0, acc);
+    }
   }
   // Merge the 4 partial states of each token: lane halves g, then waves wm.
 #pragma unroll
@@ -578,27 +616,38 @@ template <int KIND, int L2N, bool DMA>
 __global__ __launch_bounds__(kThreads) void head_dz_kernel(
     const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
     const float* __restrict__ stat, const float* __restrict__ scale, bf16* __restrict__ dz,
-    int64_t ldz, int tok0, int ntok, int d, int V, int log2n, float inv_c, float clamp) {
+    int64_t ldz, int tok0, int ntok, int d, int V, int log2n, float inv_c, float clamp,
+    int chunk_tiles) {
   GEMM_LDS_STAGES;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
   const int wm = w / NWN, wn = w % NWN;
-  const int n0 = blockIdx.x * BN;   // token offset inside the chunk
-  const int m0 = blockIdx.y * BM;   // vocabulary offset
+  const int n0 = blockIdx.x * BN;  // token offset inside the chunk
+  const int ntiles_v = (V + BM - 1) / BM;
+  const int t_begin = blockIdx.y * chunk_tiles;
+  const int t_end = min(ntiles_v, t_begin + chunk_tiles);
   const Operand A{e, d, V, d};
   const Operand B{h + (int64_t)tok0 * d, d, ntok, d};
-  Acc acc;
-  gemm_any<DMA>(A, B, m0, n0, s0, ring, acc, tid);
+  // The lane's tokens (the same for every vocabulary tile), read before the
+  // loads of the stage ring start.
+  int tgt_j[TJ];
+  float st_j[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int tl = n0 + WTN * wn + 32 * j + c32;
+    tgt_j[j] = tl < ntok ? targets[tok0 + tl] : -1;
+    st_j[j] = tl < ntok ? stat[tok0 + tl] : 0.0f;
+  }
   const float sc = scale[0];
   // FULL: every row of the tile is inside the vocabulary (all but the last
   // vocabulary tile), so no row mask is formed.
-  auto emit = [&](auto full_tag) {
+  auto emit = [&](auto full_tag, int m0, const Acc& acc) {
     constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
       const int tl = n0 + WTN * wn + 32 * j + c32;
       if (tl >= ntok) continue;
-      const int tgt = targets[tok0 + tl];
-      const float st = stat[tok0 + tl];
+      const int tgt = tgt_j[j];
+      const float st = st_j[j];
 #pragma unroll
       for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -625,10 +674,21 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
         }
     }
   };
-  if (m0 + BM <= V)
-    emit(std::true_type{});
-  else
-    emit(std::false_type{});
+  auto emit_tile = [&](int, int m0, const Acc& a) {
+    if (m0 + BM <= V)
+      emit(std::true_type{}, m0, a);
+    else
+      emit(std::false_type{}, m0, a);
+  };
+  Acc acc;
+  if constexpr (DMA) {
+    gemm_seq_dma<true, true>(A, B, t_begin * BM, t_end - t_begin, n0, ring, acc, tid, emit_tile);
+  } else {
+    for (int t = t_begin; t < t_end; ++t) {
+      gemm_tile<true, true>(A, B, t * BM, n0, s0, s0 + 2 * kStageElems, acc, tid);
+      emit_tile(t, t * BM, acc);
+    }
+  }
 }
 
 // One GEMM of a grouped launch: C[m][n] (+)= sum_k A(m,k) B(n,k).
@@ -733,9 +793,9 @@ int32_t check_head(const void* h, const void* E, const int32_t* targets, int N, 
 }
 
 typedef void (*HeadFwdFn)(const bf16*, const bf16*, const int32_t*, float*, float*, int, int,
-                          int, int, float, float);
+                          int, int, float, float, int);
 typedef void (*HeadDzFn)(const bf16*, const bf16*, const int32_t*, const float*, const float*,
-                         bf16*, int64_t, int, int, int, int, int, float, float);
+                         bf16*, int64_t, int, int, int, int, int, float, float, int);
 
 // Kernel instance for (kind, n): alg_ce with n = 8, 16 or 32 gets unrolled
 // powers. DMA (the direct-to-LDS ring) when d is a multiple of BK.
@@ -758,15 +818,26 @@ template <bool DMA> HeadDzFn pick_head_dz_as(int kind, int log2n) {
   }
 }
 HeadFwdFn pick_head_fwd(int kind, int log2n, int d) {
-  return d % BK == 0 ? pick_head_fwd_as<true>(kind, log2n) : pick_head_fwd_as<false>(kind, log2n);
+  return d % (BK * kDmaStages) == 0 ? pick_head_fwd_as<true>(kind, log2n)
+                                    : pick_head_fwd_as<false>(kind, log2n);
 }
 HeadDzFn pick_head_dz(int kind, int log2n, int d) {
-  return d % BK == 0 ? pick_head_dz_as<true>(kind, log2n) : pick_head_dz_as<false>(kind, log2n);
+  return d % (BK * kDmaStages) == 0 ? pick_head_dz_as<true>(kind, log2n)
+                                    : pick_head_dz_as<false>(kind, log2n);
 }
 
-int nchunks_of(int V) {
-  const int nt = (V + BM - 1) / BM;
-  return (nt + kVocabChunkTiles - 1) / kVocabChunkTiles;
+// Vocabulary tiles per forward workgroup: the token blocks x vocabulary tiles
+// dealt out in about kFwdWorkgroups equal chunks (one round of the CUs), so
+// no partial last round of workgroups is left.
+int chunk_tiles_of(int N, int V) {
+  const int64_t ntv = (V + BM - 1) / BM, ntb = (N + BN - 1) / BN;
+  const int64_t per = (ntv * ntb + kFwdWorkgroups - 1) / kFwdWorkgroups;
+  const int64_t nch = (ntv + per - 1) / per;
+  return (int)((ntv + nch - 1) / nch);
+}
+int nchunks_of(int N, int V) {
+  const int nt = (V + BM - 1) / BM, ct = chunk_tiles_of(N, V);
+  return (nt + ct - 1) / ct;
 }
 
 }  // namespace
@@ -778,7 +849,7 @@ extern "C" int64_t algx_head_fwd_workspace_bytes(int32_t N, int32_t d, int32_t V
   (void)d;
   if (N <= 0 || V <= 0) return 0;
   if (dtype == ALGX_F32) return head_f32_fwd_workspace(N, V);
-  return (int64_t)nchunks_of(V) * N * 2 * sizeof(float);
+  return (int64_t)nchunks_of(N, V) * N * 2 * sizeof(float);
 }
 
 extern "C" int32_t algx_head_fwd(const void* h, const void* E, const int32_t* targets,
@@ -789,7 +860,7 @@ extern "C" int32_t algx_head_fwd(const void* h, const void* E, const int32_t* ta
   if (N == 0) return 0;
   if (stat == nullptr || zt == nullptr || workspace == nullptr) return fail("head_fwd: null output");
   hipStream_t s = (hipStream_t)stream;
-  const int nch = nchunks_of(V);
+  const int nch = nchunks_of(N, V);
   dim3 grid((N + BN - 1) / BN, nch);
   const int log2n = kind == ALGX_HEAD_ALG_CE ? ilog2(n) : 0;
   float* partial = (float*)workspace;
@@ -803,7 +874,7 @@ extern "C" int32_t algx_head_fwd(const void* h, const void* E, const int32_t* ta
     const Probe probe = probe_for(ALGX_PROBE_HEAD_FWD);
     launch_k(probe, pick_head_fwd(kind, log2n, d),
              grid, dim3(kThreads), s, (const bf16*)h, (const bf16*)E, targets, zt, partial, N, d,
-             V, log2n, inv_c, clamp);
+             V, log2n, inv_c, clamp, chunk_tiles_of(N, V));
   }
   if (int32_t rc = check_launch("head_fwd")) return rc;
   const int nb = (N + 255) / 256;
@@ -843,11 +914,12 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
   const bf16* eb = (const bf16*)E;
   for (int tok0 = 0; tok0 < N; tok0 += csize) {
     const int ntok = min(csize, N - tok0);
-    dim3 gdz((ntok + BN - 1) / BN, (V + BM - 1) / BM);
+    const int ct = chunk_tiles_of(ntok, V);
+    dim3 gdz((ntok + BN - 1) / BN, ((V + BM - 1) / BM + ct - 1) / ct);
     launch_k(probe_for(ALGX_PROBE_HEAD_DZ),
              pick_head_dz(kind, log2n, d),
              gdz, dim3(kThreads), s, hb, eb, targets, stat, scale, dz, ldz, tok0, ntok, d, V, log2n,
-             inv_c, clamp);
+             inv_c, clamp, ct);
     if (int32_t rc = check_launch("head_dz")) return rc;
     // dh[t][c] = sum_v dz[t][v] E[v][c]: A = dz (k-contiguous), B(n=c,k=v) = E stored [v][c].
     // dE[v][c] (+)= sum_t dz[t][v] h[t][c]: A(m=v,k=t) = dz stored [t][v], B(n=c,k=t) = h [t][c].
