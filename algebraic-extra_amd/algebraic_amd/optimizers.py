@@ -110,14 +110,74 @@ def _ns_wide(X: torch.Tensor, steps: int, eps: float, ns_dtype: torch.dtype) -> 
     return _ns_iterate(Xn, steps)
 
 
+def gemm_bf16_batched(A: torch.Tensor, B: torch.Tensor, *, a_kc: bool, b_kc: bool,
+                      D: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """C[i] = alpha * opA(A[i]) opB(B[i])^T + beta * D[i] on libalgx's MFMA
+    GEMM core (algx_gemm_bf16_batched), bf16 in and out, float32 sums.
+
+    A, B: contiguous bf16 (k, r, c) batches. opA is A[i] itself ([M][K]) when
+    a_kc, else A[i]^T (A stored [K][M]); opB is B[i] ([N][K]) when b_kc, else
+    B[i]^T. So C = A B^T for (True, True) and C = A B for (True, False)."""
+    kb, ra, ca = A.shape
+    M, K = (ra, ca) if a_kc else (ca, ra)
+    N, Kb = (B.shape[1], B.shape[2]) if b_kc else (B.shape[2], B.shape[1])
+    if B.shape[0] != kb or Kb != K:
+        raise ValueError(f"gemm_bf16_batched: shapes {tuple(A.shape)} and {tuple(B.shape)} "
+                         "do not chain")
+    for t in (A, B) + ((D,) if D is not None else ()):
+        if t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous():
+            raise ValueError("gemm_bf16_batched: operands must be contiguous bf16 device tensors")
+    if D is not None and tuple(D.shape) != (kb, M, N):
+        raise ValueError("gemm_bf16_batched: D must be (batch, M, N)")
+    if out is None:
+        out = torch.empty((kb, M, N), dtype=torch.bfloat16, device=A.device)
+    _lib.call("algx_gemm_bf16_batched", _lib.ptr(A), _lib.ptr(B),
+              _lib.ptr(D) if D is not None else None, _lib.ptr(out), kb, M, N, K,
+              int(a_kc), int(b_kc), A.shape[2], B.shape[2], N, N, ra * ca, B.shape[1] * B.shape[2],
+              M * N, M * N, float(alpha), float(beta if D is not None else 0.0), _lib.stream())
+    return out
+
+
+def _ns_native_ok(X: torch.Tensor) -> bool:
+    m, n = X.shape[-2:]
+    return (X.is_cuda and X.dtype == torch.bfloat16 and X.is_contiguous() and
+            m % 8 == 0 and n % 8 == 0 and X.data_ptr() % 16 == 0)
+
+
 def _ns_iterate(X: torch.Tensor, steps: int) -> torch.Tensor:
     """The iteration on a normalised, contiguous batch (k, m, n), m <= n.
 
     Each update is one batched GEMM with its linear combination folded into
-    the GEMM's own alpha/beta: B = b A + c A A and X <- a X + B X
-    (= baddbmm(X, B, X, beta=a)), X <- 1.5 X - 0.5 (X X^T) X for the
-    refinements; only X X^T needs X^T materialised."""
+    the GEMM's own alpha/beta: B = b A + c A A and X <- a X + B X, and
+    X <- 1.5 X - 0.5 (X X^T) X for the refinements. bf16 device batches run
+    on libalgx's GEMM core: X X^T reads X k-contiguous on both sides (no
+    transpose is formed), A A and B X read their second operand as [k][n],
+    and every product writes a buffer of its own (no self copy)."""
     a, b, c = _NS_ABC
+    if _ns_native_ok(X):
+        k, m, n = X.shape
+        A = torch.empty((k, m, m), dtype=X.dtype, device=X.device)
+        Bm = torch.empty_like(A)
+        Xs = [X, torch.empty_like(X)]
+        cur = 0
+
+        def update(coef_mat, acc_coef, own_coef):
+            # X <- own_coef X + acc_coef (coef_mat X), into the other buffer
+            nonlocal cur
+            gemm_bf16_batched(coef_mat, Xs[cur], a_kc=True, b_kc=False, D=Xs[cur],
+                              alpha=acc_coef, beta=own_coef, out=Xs[1 - cur])
+            cur = 1 - cur
+
+        if Xs[1].data_ptr() % 16 == 0 and A.data_ptr() % 16 == 0 and Bm.data_ptr() % 16 == 0:
+            for _ in range(steps):
+                gemm_bf16_batched(Xs[cur], Xs[cur], a_kc=True, b_kc=True, out=A)
+                gemm_bf16_batched(A, A, a_kc=True, b_kc=False, D=A, alpha=c, beta=b, out=Bm)
+                update(Bm, 1.0, a)
+            for _ in range(2):
+                gemm_bf16_batched(Xs[cur], Xs[cur], a_kc=True, b_kc=True, out=A)
+                update(A, -0.5, 1.5)
+            return Xs[cur]
 
     def gram(x):
         return torch.bmm(x, _mT(x))

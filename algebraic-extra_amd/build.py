@@ -27,6 +27,7 @@ EXTRA = {
     "attn_fwd_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "attn_bwd_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "head.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "gemm_batched.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -16,418 +16,14 @@
 #include <cstdlib>
 #include <type_traits>
 
+#include "gemm_core.h"
 #include "head_f32.h"
 
 namespace algx {
 
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 32;  // output tile and k stage of every GEMM
-constexpr int LSTR = BK + 8;   // LDS row stride (bf16) of k-contiguous tiles: 80 B
-constexpr int TSTR = BM + 16;  // LDS row stride (bf16) of [k][mn] tiles: 544 B
-constexpr int NWM = 2, NWN = 4;               // waves along m and n
-constexpr int kThreads = 64 * NWM * NWN;
-constexpr int WTM = BM / NWM, WTN = BN / NWN;  // outputs per wave: 128 x 64
-constexpr int TI = WTM / 32, TJ = WTN / 32;    // 32x32 MFMA tiles per wave along m and n
-constexpr int kStageElems = BM * LSTR > BK * TSTR ? BM * LSTR : BK * TSTR;
-constexpr int kChunks = BM * BK / 8 / kThreads;  // 16-byte chunks per thread per tile stage
-static_assert(BM == BN && (BM / 8) * (kThreads / (BM / 8)) == kThreads &&
-                  kChunks * (kThreads / (BM / 8)) == BK,
-              "[k][mn] loader: BM/8 threads per k row group, kChunks k rows each");
 constexpr int kFwdWorkgroups = 256;  // forward grid target: one workgroup per CU
-
-__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// Operand of a GEMM C[m][n] = sum_k A(m,k) B(n,k). KC: stored as [MN][K]
-// (k contiguous, leading dimension ld); otherwise stored as [K][MN].
-struct Operand {
-  const bf16* p;
-  int64_t ld;
-  int rows;  // extent along m (or n)
-  int K;
-};
-
-// Stages one 256 x 64 (mn x k) tile of an operand into registers (zero
-// outside): four 16-byte loads per thread.
-// Per-thread addressing of one operand tile (set once per output tile): the
-// thread's chunks of a 256 x BK (mn x k) stage.
-template <bool KC>
-struct TileAddr {
-  const bf16* base[kChunks];  // chunk address at k stage 0 (op.p when its mn is outside)
-  int koff[kChunks];          // k of the chunk within a stage
-  bool mn_in[kChunks];
-  __device__ __forceinline__ void init(const Operand& op, int mn0, int tid) {
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-      if (KC) {
-        // [mn][k]: BK / 8 chunks per row.
-        const int id = tid + kThreads * c;
-        const int row = mn0 + id / (BK / 8);
-        koff[c] = (id % (BK / 8)) * 8;
-        mn_in[c] = row < op.rows;
-        base[c] = op.p + (mn_in[c] ? (int64_t)row * op.ld + koff[c] : 0);
-      } else {
-        // [k][mn]: kChunks consecutive k rows x 8 consecutive mn per thread.
-        const int kg = tid / (BM / 8), mg = tid % (BM / 8);
-        const int mm = mn0 + 8 * mg;
-        koff[c] = kChunks * kg + c;
-        mn_in[c] = mm < op.rows;
-        base[c] = op.p + (mn_in[c] ? (int64_t)koff[c] * op.ld + mm : 0);
-      }
-    }
-  }
-};
-
-template <bool KC>
-struct TileLoader {
-  bf16x8 r[kChunks];
-  uint32_t ok;  // bit c: chunk c is inside the operand
-  // Branch-free: an out-of-range chunk reads the operand's first 16 bytes and
-  // is replaced by zeros when stored, so no wait for the load sits here.
-  __device__ __forceinline__ void load(const Operand& op, const TileAddr<KC>& ad, int k0) {
-    ok = 0;
-    const int64_t step = KC ? (int64_t)k0 : (int64_t)k0 * op.ld;
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-      const bool in = ad.mn_in[c] && k0 + ad.koff[c] < op.K;
-      ok |= in ? 1u << c : 0u;
-      r[c] = *reinterpret_cast<const bf16x8*>(in ? ad.base[c] + step : op.p);
-    }
-  }
-  __device__ __forceinline__ void store(bf16* lds, int tid) const {
-    if (KC) {
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c) {
-        const int id = tid + kThreads * c;
-        *reinterpret_cast<bf16x8*>(lds + (id / (BK / 8)) * LSTR + (id % (BK / 8)) * 8) =
-            (ok >> c) & 1 ? r[c] : bf16x8{};
-      }
-    } else {
-      // Kept as stored in memory, [k][mn]; the MFMA operand is read through
-      // transposing LDS reads.
-      const int kg = tid / (BM / 8), mg = tid % (BM / 8);
-#pragma unroll
-      for (int i = 0; i < kChunks; ++i)
-        *reinterpret_cast<bf16x8*>(lds + (kChunks * kg + i) * TSTR + 8 * mg) =
-            (ok >> i) & 1 ? r[i] : bf16x8{};
-    }
-  }
-};
-
-typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-
-// MFMA operand (rows mn0 + (lane % 32), k-slots k0 + 8(lane / 32) .. +7) of a
-// tile in LDS: one 16-byte read from a [mn][k] tile, or two transposing reads
-// (ds_read_b64_tr_b16) from a [k][mn] tile, in which lane 4j+m of each
-// 16-lane group addresses row j, columns 4m .. 4m+3.
-template <bool KC>
-__device__ __forceinline__ bf16x8 operand(const bf16* tile, int mn0, int k0, int lane) {
-  if (KC) {
-    return *reinterpret_cast<const bf16x8*>(tile + (mn0 + (lane & 31)) * LSTR + k0 + 8 * (lane >> 5));
-  } else {
-    const int G = lane >> 4, j = (lane >> 2) & 3, m = lane & 3;
-    const bf16* p = tile + (k0 + 8 * (G >> 1) + j) * TSTR + mn0 + 16 * (G & 1) + 4 * m;
-    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
-    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * TSTR));
-    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  }
-}
-
-// Wave w = (wm, wn) = (w / NWN, w % NWN) owns outputs m0 + WTM wm .. + WTM - 1,
-// n0 + WTN wn .. + WTN - 1:
-// acc.v[i][j][r] = C[m0 + WTM wm + 32i + 8(r/4) + 4g + r%4][n0 + WTN wn + 32j + c32].
-struct Acc {
-  f32x16 v[TI][TJ];
-  __device__ __forceinline__ void zero() {
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-      for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[i][j][r] = 0.0f;
-  }
-};
-
-template <bool AKC, bool BKC>
-__device__ __forceinline__ void mma_stage(const bf16* As, const bf16* Bs, Acc& acc, int wm,
-                                          int wn, int lane) {
-#pragma unroll
-  for (int ks = 0; ks < BK / 16; ++ks) {
-    bf16x8 a[TI], b[TJ];
-#pragma unroll
-    for (int i = 0; i < TI; ++i) a[i] = operand<AKC>(As, WTM * wm + 32 * i, 16 * ks, lane);
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) b[j] = operand<BKC>(Bs, WTN * wn + 32 * j, 16 * ks, lane);
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) acc.v[i][j] = mfma32(a[i], b[j], acc.v[i][j]);
-  }
-}
-
-// Full-K product of one output tile: LDS double-buffered, global loads two
-// k stages ahead (two register sets, so a stage's HBM latency spans two
-// stages of MFMA work).
-template <bool AKC, bool BKC>
-__device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int m0, int n0,
-                                          bf16* As, bf16* Bs, Acc& acc, int tid) {
-  const int w = tid >> 6, lane = tid & 63;
-  const int wm = w / NWN, wn = w % NWN;
-  const int K = A.K;
-  const int nk = (K + BK - 1) / BK;
-  TileAddr<AKC> aa;
-  TileAddr<BKC> ab;
-  aa.init(A, m0, tid);
-  ab.init(B, n0, tid);
-  TileLoader<AKC> la0, la1;
-  TileLoader<BKC> lb0, lb1;
-  acc.zero();
-  // Every step issues the same loads (stage indices past the end are clamped
-  // to the last stage and never stored), so each wait before a store covers
-  // exactly the loads of the stage it stores.
-  const int klast = (nk - 1) * BK;
-  la0.load(A, aa, 0);
-  lb0.load(B, ab, 0);
-  la1.load(A, aa, min(BK, klast));
-  lb1.load(B, ab, min(BK, klast));
-  __syncthreads();  // previous users of the LDS buffers are done
-  la0.store(As, tid);
-  lb0.store(Bs, tid);
-  __syncthreads();
-  // Stage kk sits in LDS buffer kk % 2; register set kk % 2 held it and is
-  // refilled with stage kk + 2 while stage kk + 1 waits in the other set.
-  auto step = [&](int kk, TileLoader<AKC>& la_cur, TileLoader<BKC>& lb_cur,
-                  TileLoader<AKC>& la_nxt, TileLoader<BKC>& lb_nxt) {
-    const int buf = kk & 1;
-    la_cur.load(A, aa, min((kk + 2) * BK, klast));
-    lb_cur.load(B, ab, min((kk + 2) * BK, klast));
-    mma_stage<AKC, BKC>(As + buf * kStageElems, Bs + buf * kStageElems, acc, wm, wn, lane);
-    if (kk + 1 < nk) {
-      la_nxt.store(As + (buf ^ 1) * kStageElems, tid);
-      lb_nxt.store(Bs + (buf ^ 1) * kStageElems, tid);
-    }
-    __syncthreads();
-  };
-  for (int kk = 0; kk < nk; kk += 2) {
-    step(kk, la0, lb0, la1, lb1);
-    if (kk + 1 < nk) step(kk + 1, la1, lb1, la0, lb0);
-  }
-}
-
-// ------------------------------------------------ direct-to-LDS GEMM core
-// The same product with the stages moved from memory straight into LDS by
-// LDS-DMA loads (global_load_lds_dwordx4: lane i of a wave's load writes its
-// 16 bytes at the destination + 16 i), so no registers stage them and no LDS
-// stores are issued; a ring of four stages keeps the loads two stages ahead
-// of the operand reads, with one barrier per stage. Stages are unpadded, with their
-// 16-byte chunks XOR-permuted so that the operand reads meet every LDS bank
-// once per pass: [mn][k] tiles (64-byte rows) keep chunk c of row r at
-// c ^ ((r >> 2) & 3), [k][mn] tiles (512-byte rows) at c ^ 4 (r & 3). Needs
-// K % BK == 0 (no partial stage); rows (or columns) past the operand's extent
-// load the operand's first bytes, which only reach outputs that are never
-// stored.
-constexpr int kDmaStages = 4;
-constexpr int kDmaOpElems = BM * BK;            // one operand stage: 8192 bf16
-
-// Source of this lane's 16 bytes in 1 KB block `blk` of a stage at k = 0.
-template <bool KC>
-__device__ __forceinline__ const bf16* dma_src(const Operand& op, int mn0, int blk, int lane) {
-  if (KC) {
-    const int r = 16 * blk + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
-    const int row = mn0 + r;
-    return row < op.rows ? op.p + (int64_t)row * op.ld + 8 * c : op.p;
-  } else {
-    const int r = 2 * blk + (lane >> 5), c = (lane & 31) ^ (4 * (r & 3));
-    const int col = mn0 + 8 * c;
-    return col < op.rows ? op.p + (int64_t)r * op.ld + col : op.p;
-  }
-}
-
-// MFMA operand (as `operand`) from a swizzled DMA stage.
-template <bool KC>
-__device__ __forceinline__ bf16x8 operand_dma(const bf16* tile, int mn0, int k0, int lane) {
-  if (KC) {
-    const int r = mn0 + (lane & 31), c = (k0 >> 3) + (lane >> 5);
-    return *reinterpret_cast<const bf16x8*>(tile + r * BK + 8 * (c ^ ((r >> 2) & 3)));
-  } else {
-    const int G = lane >> 4, j = (lane >> 2) & 3, m = lane & 3;
-    const int r = k0 + 8 * (G >> 1) + j;
-    const int col = mn0 + 16 * (G & 1) + 4 * m;
-    const bf16* p = tile + r * BM + 8 * ((col >> 3) ^ (4 * (r & 3))) + (col & 7);
-    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
-    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * BM));
-    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  }
-}
-
-// One LDS-DMA load of a wave: lane i's 16 bytes at src go to dst + 16 i (dst
-// wave-uniform). Issued as inline assembly so that the compiler does not
-// track it: its waitcnt pass cannot tell which LDS buffer such a load writes
-// and would wait for all of them before every LDS read; the ring below waits
-// for its own loads explicitly (wait_vm) before the barrier that publishes
-// them.
-__device__ __forceinline__ void dma16(const bf16* src, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
-               : "memory", "m0");
-}
-
-// s_waitcnt immediates: vmcnt(n) with expcnt and lgkmcnt unconstrained.
-template <int N> __device__ __forceinline__ void wait_vm() {
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
-}
-
-// Ring of stage buffers (32 KB each: the A stage, then the B stage).
-struct DmaRing {
-  bf16* slot[kDmaStages];
-};
-
-// LDS byte address of a pointer into a __shared__ array.
-__device__ __forceinline__ unsigned lds_addr(const void* p) {
-  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// Products of `ntiles` output tiles that share the B rows n0: tile t uses A
-// rows m0 + t BM; epi(t, m0 + t BM, acc) receives each finished tile. The
-// ring streams across the tiles, so a tile's first stages load during the
-// previous tile's last stages and epilogue. Several tiles need the tile's
-// stage count to be a multiple of the ring's (every tile starts at slot 0).
-template <bool AKC, bool BKC, typename Epi>
-__device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B, int m0,
-                                             int ntiles, int n0, const DmaRing& ring, Acc& acc,
-                                             int tid, Epi&& epi) {
-  constexpr int S = kDmaStages, L = S - 2;  // stages in flight beyond the one being read
-  const int w = tid >> 6, lane = tid & 63;
-  const int wm = w / NWN, wn = w % NWN;
-  const int nk = A.K / BK;
-  const int G = ntiles * nk;  // stages of the whole sequence
-  const bf16* sa0 = dma_src<AKC>(A, m0, 2 * w, lane);  // A sources of the tile being issued
-  const bf16* sa1 = dma_src<AKC>(A, m0, 2 * w + 1, lane);
-  const bf16* sb0 = dma_src<BKC>(B, n0, 2 * w, lane);
-  const bf16* sb1 = dma_src<BKC>(B, n0, 2 * w + 1, lane);
-  const int64_t stepA = AKC ? BK : (int64_t)BK * A.ld;
-  const int64_t stepB = BKC ? BK : (int64_t)BK * B.ld;
-  // Byte offset of the wave's two 1 KB blocks in an operand stage (uniform).
-  const unsigned wofs = 2048u * __builtin_amdgcn_readfirstlane(w);
-  // The wave's two 1 KB blocks of each operand of stage kk (A sources a0/a1)
-  // -> slot.
-  auto issue = [&](const bf16* a0, const bf16* a1, int kk, bf16* slot) {
-    const unsigned dA = lds_addr(slot) + wofs, dB = dA + 2 * kDmaOpElems;
-    // Stage offsets as scalars computed here (the compiler would otherwise
-    // keep one vector induction variable per unrolled stage).
-    int64_t oa = kk * stepA, ob = kk * stepB;
-    asm volatile("" : "+s"(oa), "+s"(ob));
-    dma16(a0 + oa, dA);
-    dma16(a1 + oa, dA + 1024);
-    dma16(sb0 + ob, dB);
-    dma16(sb1 + ob, dB + 1024);
-  };
-  // Wait until at most `later` of this wave's stages are still loading (four
-  // loads a stage; the loads complete in issue order, and any later vector
-  // memory operation only makes the wait stricter).
-  auto wait_stages = [](int later) {
-    static_assert(L <= 4, "the vmcnt immediates below cover up to three later stages");
-    if (later <= 0)
-      wait_vm<0>();
-    else if (later == 1)
-      wait_vm<4>();
-    else if (later == 2)
-      wait_vm<8>();
-    else
-      wait_vm<12>();
-  };
-  // Operands of one 16-wide k step (ks) of a stage into registers.
-  auto rd = [&](const bf16* As, int ks, bf16x8 (&a)[TI], bf16x8 (&b)[TJ]) {
-    const bf16* Bs = As + kDmaOpElems;
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) b[j] = operand_dma<BKC>(Bs, WTN * wn + 32 * j, 16 * ks, lane);
-#pragma unroll
-    for (int i = 0; i < TI; ++i) a[i] = operand_dma<AKC>(As, WTM * wm + 32 * i, 16 * ks, lane);
-  };
-  auto mm = [&](const bf16x8 (&a)[TI], const bf16x8 (&b)[TJ]) {
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) acc.v[i][j] = mfma32(a[i], b[j], acc.v[i][j]);
-  };
-  acc.zero();
-  wait_vm<0>();     // nothing older is counted with the ring's loads
-  __syncthreads();  // previous users of the ring are done
-  // Stages 0 .. S-2 now (all of the first tile when there are several), then
-  // stage g + S - 1 at the barrier of stage g (into the slot of stage g - 1),
-  // so every stage is issued two stages before its operands are read.
-#pragma unroll
-  for (int u = 0; u < S - 1; ++u)
-    if (u < nk) issue(sa0, sa1, u, ring.slot[u]);
-  wait_stages(min(S - 2, G - 1));
-  __syncthreads();
-  // Register double buffer over half stages: the operands of the next half
-  // stage are read while the MFMAs of the current one run. The barrier sits
-  // between a stage's halves: it publishes stage g + 1 (whose first half is
-  // read next). It does not wait for this wave's LDS reads: those in flight
-  // read the slot of stage g, which no load refills before the next barrier.
-  // On the last stage the reads of "stage G" fetch a stale slot and are unused.
-  bf16x8 xa[TI], xb[TJ], ya[TI], yb[TJ];
-  rd(ring.slot[0], 0, xa, xb);
-  for (int t = 0; t < ntiles; ++t) {
-    // A sources of the next tile, for the stages issued near this tile's end.
-    const bf16* na0 = sa0;
-    const bf16* na1 = sa1;
-    if (t + 1 < ntiles) {
-      na0 = dma_src<AKC>(A, m0 + (t + 1) * BM, 2 * w, lane);
-      na1 = dma_src<AKC>(A, m0 + (t + 1) * BM, 2 * w + 1, lane);
-    }
-    const int g0 = t * nk;
-    auto step = [&](int kk, const bf16* cur, const bf16* nxt, bf16* refill) {
-      rd(cur, 1, ya, yb);
-      __builtin_amdgcn_sched_barrier(0);
-      mm(xa, xb);
-      __builtin_amdgcn_sched_barrier(0);
-      // Wait for stage g + 1; the stages issued after it may stay in flight.
-      const int g = g0 + kk;
-      wait_stages(min(g + S - 2, G - 1) - (g + 1));
-      asm volatile("s_barrier" ::: "memory");
-      if (kk + S - 1 < nk)
-        issue(sa0, sa1, kk + S - 1, refill);
-      else if (t + 1 < ntiles)
-        issue(na0, na1, kk + S - 1 - nk, refill);
-      rd(nxt, 0, xa, xb);
-      __builtin_amdgcn_sched_barrier(0);
-      mm(ya, yb);
-    };
-    // Slots are named statically: S stages a turn.
-    for (int kk = 0; kk < nk; kk += S) {
-#pragma unroll
-      for (int u = 0; u < S; ++u)
-        if (kk + u < nk)
-          step(kk + u, ring.slot[u], ring.slot[(u + 1) % S], ring.slot[(u + S - 1) % S]);
-    }
-    epi(t, m0 + t * BM, acc);
-    acc.zero();
-    sa0 = na0;
-    sa1 = na1;
-  }
-}
-
-// Full-K product of one output tile on the direct-to-LDS ring.
-template <bool AKC, bool BKC>
-__device__ __forceinline__ void gemm_tile_dma(const Operand& A, const Operand& B, int m0, int n0,
-                                              const DmaRing& ring, Acc& acc, int tid) {
-  Acc out;
-  gemm_seq_dma<AKC, BKC>(A, B, m0, 1, n0, ring, out, tid,
-                         [&](int, int, Acc& a) { acc = a; });
-}
-
-// LDS of a kernel built on the GEMM cores (DMA: a compile-time bool in
-// scope): four 32 KB stage buffers of the direct-to-LDS ring, or the two
-// double-buffered operand stages of gemm_tile in the first of them.
-#define GEMM_LDS_STAGES                                                                  \
-  __shared__ __attribute__((aligned(16))) bf16 s0[DMA ? 2 * kDmaOpElems : 4 * kStageElems]; \
-  __shared__ __attribute__((aligned(16))) bf16 s1[DMA ? 2 * kDmaOpElems : 8];               \
-  __shared__ __attribute__((aligned(16))) bf16 s2[DMA ? 2 * kDmaOpElems : 8];               \
-  __shared__ __attribute__((aligned(16))) bf16 s3[DMA ? 2 * kDmaOpElems : 8];               \
-  const DmaRing ring{{s0, s1, s2, s3}}
 
 // x^n, n = 2^log2n: unrolled squarings for a compile-time L2N > 0 (a runtime
 // loop inside the per-logit epilogue would cost a branch per logit).
@@ -729,19 +325,6 @@ __device__ __forceinline__ void gemm_job(const GemmJob& jb, int tile, bf16* lds,
           *dst = from_f<TOut>(acc.v[i][j][r]);
       }
     }
-}
-
-// XCD-aware tile order of a grouped GEMM: workgroups are dealt to the 8 XCDs
-// round-robin by index, so the tiles_n output tiles that share one row block
-// of A (one dz block) go to indices 8 apart, i.e. to one XCD and its L2, and
-// run at about the same time. Index `b` counts from a multiple of 8; a
-// trailing partial group keeps the plain order.
-__device__ __forceinline__ int xcd_tile(int b, int ntiles, int tiles_n) {
-  const int grp = 8 * tiles_n;
-  const int full = ntiles / grp * grp;
-  if (b >= full) return b;
-  const int r = b % grp;
-  return ((b / grp) * 8 + (r & 7)) * tiles_n + (r >> 3);
 }
 
 // The backward's two products of a token chunk in one launch (the long-K dh

@@ -323,6 +323,21 @@ int32_t algx_adamw_step(float* p, const float* g, float* m, float* v, int64_t n,
 int64_t algx_ns_normalize_workspace_bytes(int64_t K, int64_t MN);
 int32_t algx_ns_normalize(const float* x, void* out, int64_t K, int64_t MN, int32_t out_dtype,
                           float eps, void* workspace, void* stream);
+/* algx_gemm_bf16_batched: the products of newton_schulz_5's iteration
+ * (src/algebraic/optimizers.py:46-60: A = X X^T, B = b A + c A A,
+ * X <- a X + B X, and the refinements X <- 1.5 X - 0.5 (X X^T) X), as a
+ * batched bf16 GEMM with the linear combination fused:
+ *   C[i] = alpha * sum_k opA(m, k) opB(n, k) + beta * D[i]   (float32 sums)
+ * over `batch` matrices (operand i at base + i * stride). opA(m, k) is
+ * A[m*lda + k] when a_kc (k-contiguous) else A[k*lda + m]; opB(n, k)
+ * likewise with ldb and b_kc. C and D (optional: null skips beta) are
+ * row-major [M][N] with ldc / ldd; D may be C. bf16 throughout; M, N, K,
+ * leading dimensions and strides multiples of 8, pointers 16-byte aligned. */
+int32_t algx_gemm_bf16_batched(const void* A, const void* B, const void* D, void* C,
+                               int32_t batch, int32_t M, int32_t N, int32_t K, int32_t a_kc,
+                               int32_t b_kc, int64_t lda, int64_t ldb, int64_t ldd, int64_t ldc,
+                               int64_t stride_a, int64_t stride_b, int64_t stride_d,
+                               int64_t stride_c, float alpha, float beta, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,80 @@
+"""algx_gemm_bf16_batched (the Newton-Schulz products, optimizers.py:46-60)
+against a float32 torch reference of the same bf16 inputs."""
+
+import pytest
+import torch
+
+from algebraic_amd import optimizers as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _ref(A, B, a_kc, b_kc, D, alpha, beta):
+    a = A.float() if a_kc else A.float().transpose(1, 2)
+    b = B.float() if b_kc else B.float().transpose(1, 2)
+    c = alpha * torch.bmm(a, b.transpose(1, 2).contiguous())
+    return c + beta * D.float() if D is not None else c
+
+
+def _check(got, want):
+    err = (got.float() - want).abs().max().item()
+    scale = want.abs().max().item()
+    # bf16 output rounding (2^-8 relative) on float32 sums of bf16 products
+    assert err <= 8e-3 * scale + 1e-3, (err, scale)
+
+
+@pytest.mark.parametrize("a_kc,b_kc", [(True, True), (True, False), (False, True), (False, False)])
+@pytest.mark.parametrize("batch,M,N,K", [(3, 264, 520, 96), (8, 256, 256, 1024), (2, 40, 8, 72),
+                                         (5, 520, 264, 200)])
+def test_batched_gemm_layouts(a_kc, b_kc, batch, M, N, K):
+    """Ragged tiles (M, N not multiples of 256), K a multiple of 32 (direct-to-
+    LDS stages) or only of 8 (register-staged stages), batches that do and do
+    not take the XCD-grouped workgroup order, every operand layout."""
+    g = torch.Generator(device=DEV).manual_seed(M + N + K)
+    A = torch.randn((batch, M, K) if a_kc else (batch, K, M), generator=g, device=DEV).bfloat16()
+    B = torch.randn((batch, N, K) if b_kc else (batch, K, N), generator=g, device=DEV).bfloat16()
+    D = torch.randn((batch, M, N), generator=g, device=DEV).bfloat16()
+    got = O.gemm_bf16_batched(A, B, a_kc=a_kc, b_kc=b_kc, D=D, alpha=-0.5, beta=1.5)
+    _check(got, _ref(A, B, a_kc, b_kc, D, -0.5, 1.5))
+    got = O.gemm_bf16_batched(A, B, a_kc=a_kc, b_kc=b_kc)
+    _check(got, _ref(A, B, a_kc, b_kc, None, 1.0, 0.0))
+
+
+def test_batched_gemm_in_place_combination():
+    """D may be the output itself (each element is read before it is written)."""
+    g = torch.Generator(device=DEV).manual_seed(7)
+    A = torch.randn((4, 128, 256), generator=g, device=DEV).bfloat16()
+    C = torch.randn((4, 128, 128), generator=g, device=DEV).bfloat16()
+    want = _ref(A, A, True, True, C, 2.0315, -4.775)
+    O.gemm_bf16_batched(A, A, a_kc=True, b_kc=True, D=C, alpha=2.0315, beta=-4.775, out=C)
+    _check(C, want)
+
+
+def test_batched_gemm_rejects_bad_shapes():
+    A = torch.zeros((2, 12, 16), device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="multiples of 8"):
+        O.gemm_bf16_batched(A, A, a_kc=True, b_kc=True)
+    with pytest.raises(ValueError, match="do not chain"):
+        O.gemm_bf16_batched(A, torch.zeros((2, 8, 24), device=DEV, dtype=torch.bfloat16),
+                            a_kc=True, b_kc=True)
+
+
+def test_newton_schulz_products_match_torch_iteration():
+    """The native iteration against the same iteration on torch bmm/baddbmm
+    (float32 sums of the same bf16 products), at the model's wide shape."""
+    g = torch.Generator(device=DEV).manual_seed(3)
+    G = torch.randn((8, 1024, 2688), generator=g, device=DEV)
+    X = torch.empty(G.shape, dtype=torch.bfloat16, device=DEV)
+    O._normalize_into(G, X, 1e-7)
+    got = O._ns_iterate(X.clone(), 5)
+    a, b, c = O._NS_ABC
+    Y = X.clone()
+    for _ in range(5):
+        A = torch.bmm(Y, Y.transpose(1, 2).contiguous())
+        Bm = torch.baddbmm(A, A, A, beta=b, alpha=c)
+        Y = torch.baddbmm(Y, Bm, Y, beta=a, alpha=1.0)
+    for _ in range(2):
+        Y = torch.baddbmm(Y, torch.bmm(Y, Y.transpose(1, 2).contiguous()), Y, beta=1.5, alpha=-0.5)
+    rel = ((got.float() - Y.float()).norm() / Y.float().norm()).item()
+    assert rel <= 2e-2, rel
