@@ -82,7 +82,7 @@ SIGNATURES = {
     "algx_adamw_step": (_i32, [_p, _p, _p, _p, _i64, _f32, _f32, _f32, _f32, _f32, _f32, _f32, _p]),
     "algx_ns_normalize_workspace_bytes": (_i64, [_i64, _i64]),
     "algx_ns_normalize": (_i32, [_p, _p, _i64, _i64, _i32, _f32, _p, _p]),
-    "algx_gemm_bf16_batched": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
+    "algx_gemm_bf16_batched": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                       _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                       _f32, _f32, _p]),
     "algx_qk_prologue_fwd": (_i32, [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,

@@ -112,13 +112,15 @@ def _ns_wide(X: torch.Tensor, steps: int, eps: float, ns_dtype: torch.dtype) -> 
 
 def gemm_bf16_batched(A: torch.Tensor, B: torch.Tensor, *, a_kc: bool, b_kc: bool,
                       D: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0,
-                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      out: Optional[torch.Tensor] = None, symmetric: bool = False) -> torch.Tensor:
     """C[i] = alpha * opA(A[i]) opB(B[i])^T + beta * D[i] on libalgx's MFMA
     GEMM core (algx_gemm_bf16_batched), bf16 in and out, float32 sums.
 
     A, B: contiguous bf16 (k, r, c) batches. opA is A[i] itself ([M][K]) when
     a_kc, else A[i]^T (A stored [K][M]); opB is B[i] ([N][K]) when b_kc, else
-    B[i]^T. So C = A B^T for (True, True) and C = A B for (True, False)."""
+    B[i]^T. So C = A B^T for (True, True) and C = A B for (True, False).
+    ``symmetric`` states that C is symmetric (the product and D): only the
+    tiles on and above the diagonal are formed, then mirrored."""
     kb, ra, ca = A.shape
     M, K = (ra, ca) if a_kc else (ca, ra)
     N, Kb = (B.shape[1], B.shape[2]) if b_kc else (B.shape[2], B.shape[1])
@@ -134,7 +136,8 @@ def gemm_bf16_batched(A: torch.Tensor, B: torch.Tensor, *, a_kc: bool, b_kc: boo
         out = torch.empty((kb, M, N), dtype=torch.bfloat16, device=A.device)
     _lib.call("algx_gemm_bf16_batched", _lib.ptr(A), _lib.ptr(B),
               _lib.ptr(D) if D is not None else None, _lib.ptr(out), kb, M, N, K,
-              int(a_kc), int(b_kc), A.shape[2], B.shape[2], N, N, ra * ca, B.shape[1] * B.shape[2],
+              int(a_kc), int(b_kc), int(symmetric), A.shape[2], B.shape[2], N, N, ra * ca,
+              B.shape[1] * B.shape[2],
               M * N, M * N, float(alpha), float(beta if D is not None else 0.0), _lib.stream())
     return out
 
@@ -170,12 +173,14 @@ def _ns_iterate(X: torch.Tensor, steps: int) -> torch.Tensor:
             cur = 1 - cur
 
         if Xs[1].data_ptr() % 16 == 0 and A.data_ptr() % 16 == 0 and Bm.data_ptr() % 16 == 0:
+            # X X^T and b A + c A A are symmetric: upper-triangle tiles only
             for _ in range(steps):
-                gemm_bf16_batched(Xs[cur], Xs[cur], a_kc=True, b_kc=True, out=A)
-                gemm_bf16_batched(A, A, a_kc=True, b_kc=False, D=A, alpha=c, beta=b, out=Bm)
+                gemm_bf16_batched(Xs[cur], Xs[cur], a_kc=True, b_kc=True, out=A, symmetric=True)
+                gemm_bf16_batched(A, A, a_kc=True, b_kc=False, D=A, alpha=c, beta=b, out=Bm,
+                                  symmetric=True)
                 update(Bm, 1.0, a)
             for _ in range(2):
-                gemm_bf16_batched(Xs[cur], Xs[cur], a_kc=True, b_kc=True, out=A)
+                gemm_bf16_batched(Xs[cur], Xs[cur], a_kc=True, b_kc=True, out=A, symmetric=True)
                 update(A, -0.5, 1.5)
             return Xs[cur]
 
@@ -214,7 +219,7 @@ def newton_schulz_many(Gs, steps: int = 5, eps: float = 1e-7,
     """newton_schulz_5 of every tensor in Gs, the matrices of equal (oriented)
     shape run as one batch: the model's 7 stacked weights become two batches
     ([w_q | w_k | w_v | w_o] and [w_g | w_u | w_d^T])."""
-    return [(y.to(F32) * sc).reshape(G.shape)
+    return [(y.to(F32) * sc if sc != 1.0 else y.to(F32)).reshape(G.shape)
             for G, (y, sc) in zip(Gs, _newton_schulz_unscaled(Gs, steps, eps, ns_dtype))]
 
 

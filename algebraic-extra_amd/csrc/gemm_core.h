@@ -215,7 +215,10 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 // K % BK == 0 (no partial stage); rows (or columns) past the operand's extent
 // load the operand's first bytes, which only reach outputs that are never
 // stored.
-constexpr int kDmaStages = 4;
+#ifndef ALGX_DMA_SLOTS
+#define ALGX_DMA_SLOTS 4
+#endif
+constexpr int kDmaStages = ALGX_DMA_SLOTS;
 constexpr int kDmaOpElems = BM * BK;            // one operand stage: 8192 bf16
 
 // Source of this lane's 16 bytes in 1 KB block `blk` of a stage at k = 0.
@@ -267,7 +270,7 @@ template <int N> __device__ __forceinline__ void wait_vm() {
 
 // Ring of stage buffers (32 KB each: the A stage, then the B stage).
 struct DmaRing {
-  bf16* slot[kDmaStages];
+  bf16* slot[5];
 };
 
 // LDS byte address of a pointer into a __shared__ array.
@@ -275,31 +278,29 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
   return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// Products of `ntiles` output tiles that share the B rows n0: tile t uses A
-// rows m0 + t BM; epi(t, m0 + t BM, acc) receives each finished tile. The
-// ring streams across the tiles, so a tile's first stages load during the
-// previous tile's last stages and epilogue. Several tiles need the tile's
-// stage count to be a multiple of the ring's (every tile starts at slot 0).
-template <bool AKC, bool BKC, typename Epi>
-__device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B, int m0,
-                                             int ntiles, int n0, const DmaRing& ring, Acc& acc,
-                                             int tid, Epi&& epi) {
+// Products of a sequence of `ntiles` output tiles with nk k stages each:
+// src(t, a0, a1, b0, b1) gives the wave's four LDS-DMA sources of tile t at
+// k = 0 (dma_src of its A and B blocks 2w and 2w + 1; the operands' k steps
+// stepA / stepB are the same for every tile), epi(t, acc) receives each
+// finished tile. The ring streams across the tiles, so a tile's first stages
+// load during the previous tile's last stages and epilogue. Several tiles
+// need nk to be a multiple of the ring's stage count (every tile starts at
+// slot 0).
+template <bool AKC, bool BKC, typename Src, typename Epi>
+__device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t stepB, int ntiles,
+                                                Src&& src, const DmaRing& ring, Acc& acc,
+                                                int tid, Epi&& epi) {
   constexpr int S = kDmaStages, L = S - 2;  // stages in flight beyond the one being read
   const int w = tid >> 6, lane = tid & 63;
   const int wm = w / NWN, wn = w % NWN;
-  const int nk = A.K / BK;
   const int G = ntiles * nk;  // stages of the whole sequence
-  const bf16* sa0 = dma_src<AKC>(A, m0, 2 * w, lane);  // A sources of the tile being issued
-  const bf16* sa1 = dma_src<AKC>(A, m0, 2 * w + 1, lane);
-  const bf16* sb0 = dma_src<BKC>(B, n0, 2 * w, lane);
-  const bf16* sb1 = dma_src<BKC>(B, n0, 2 * w + 1, lane);
-  const int64_t stepA = AKC ? BK : (int64_t)BK * A.ld;
-  const int64_t stepB = BKC ? BK : (int64_t)BK * B.ld;
+  const bf16 *sa0, *sa1, *sb0, *sb1;  // sources of the tile being issued
+  src(0, sa0, sa1, sb0, sb1);
   // Byte offset of the wave's two 1 KB blocks in an operand stage (uniform).
   const unsigned wofs = 2048u * __builtin_amdgcn_readfirstlane(w);
-  // The wave's two 1 KB blocks of each operand of stage kk (A sources a0/a1)
-  // -> slot.
-  auto issue = [&](const bf16* a0, const bf16* a1, int kk, bf16* slot) {
+  // The wave's two 1 KB blocks of each operand of stage kk -> slot.
+  auto issue = [&](const bf16* a0, const bf16* a1, const bf16* b0, const bf16* b1, int kk,
+                   bf16* slot) {
     const unsigned dA = lds_addr(slot) + wofs, dB = dA + 2 * kDmaOpElems;
     // Stage offsets as scalars computed here (the compiler would otherwise
     // keep one vector induction variable per unrolled stage).
@@ -307,8 +308,8 @@ __device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B,
     asm volatile("" : "+s"(oa), "+s"(ob));
     dma16(a0 + oa, dA);
     dma16(a1 + oa, dA + 1024);
-    dma16(sb0 + ob, dB);
-    dma16(sb1 + ob, dB + 1024);
+    dma16(b0 + ob, dB);
+    dma16(b1 + ob, dB + 1024);
   };
   // Wait until at most `later` of this wave's stages are still loading (four
   // loads a stage; the loads complete in issue order, and any later vector
@@ -346,7 +347,7 @@ __device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B,
   // so every stage is issued two stages before its operands are read.
 #pragma unroll
   for (int u = 0; u < S - 1; ++u)
-    if (u < nk) issue(sa0, sa1, u, ring.slot[u]);
+    if (u < nk) issue(sa0, sa1, sb0, sb1, u, ring.slot[u]);
   wait_stages(min(S - 2, G - 1));
   __syncthreads();
   // Register double buffer over half stages: the operands of the next half
@@ -358,13 +359,9 @@ __device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B,
   bf16x8 xa[TI], xb[TJ], ya[TI], yb[TJ];
   rd(ring.slot[0], 0, xa, xb);
   for (int t = 0; t < ntiles; ++t) {
-    // A sources of the next tile, for the stages issued near this tile's end.
-    const bf16* na0 = sa0;
-    const bf16* na1 = sa1;
-    if (t + 1 < ntiles) {
-      na0 = dma_src<AKC>(A, m0 + (t + 1) * BM, 2 * w, lane);
-      na1 = dma_src<AKC>(A, m0 + (t + 1) * BM, 2 * w + 1, lane);
-    }
+    // Sources of the next tile, for the stages issued near this tile's end.
+    const bf16 *na0 = sa0, *na1 = sa1, *nb0 = sb0, *nb1 = sb1;
+    if (t + 1 < ntiles) src(t + 1, na0, na1, nb0, nb1);
     const int g0 = t * nk;
     auto step = [&](int kk, const bf16* cur, const bf16* nxt, bf16* refill) {
       rd(cur, 1, ya, yb);
@@ -376,9 +373,9 @@ __device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B,
       wait_stages(min(g + S - 2, G - 1) - (g + 1));
       asm volatile("s_barrier" ::: "memory");
       if (kk + S - 1 < nk)
-        issue(sa0, sa1, kk + S - 1, refill);
+        issue(sa0, sa1, sb0, sb1, kk + S - 1, refill);
       else if (t + 1 < ntiles)
-        issue(na0, na1, kk + S - 1 - nk, refill);
+        issue(na0, na1, nb0, nb1, kk + S - 1 - nk, refill);
       rd(nxt, 0, xa, xb);
       __builtin_amdgcn_sched_barrier(0);
       mm(ya, yb);
@@ -390,11 +387,33 @@ __device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B,
         if (kk + u < nk)
           step(kk + u, ring.slot[u], ring.slot[(u + 1) % S], ring.slot[(u + S - 1) % S]);
     }
-    epi(t, m0 + t * BM, acc);
+    epi(t, acc);
     acc.zero();
     sa0 = na0;
     sa1 = na1;
+    sb0 = nb0;
+    sb1 = nb1;
   }
+}
+
+// Products of `ntiles` output tiles that share the B rows n0: tile t uses A
+// rows m0 + t BM; epi(t, m0 + t BM, acc) receives each finished tile.
+template <bool AKC, bool BKC, typename Epi>
+__device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B, int m0,
+                                             int ntiles, int n0, const DmaRing& ring, Acc& acc,
+                                             int tid, Epi&& epi) {
+  const int w = tid >> 6, lane = tid & 63;
+  const bf16* b0 = dma_src<BKC>(B, n0, 2 * w, lane);
+  const bf16* b1 = dma_src<BKC>(B, n0, 2 * w + 1, lane);
+  gemm_stream_dma<AKC, BKC>(
+      A.K / BK, AKC ? BK : (int64_t)BK * A.ld, BKC ? BK : (int64_t)BK * B.ld, ntiles,
+      [&](int t, const bf16*& a0, const bf16*& a1, const bf16*& sb0, const bf16*& sb1) {
+        a0 = dma_src<AKC>(A, m0 + t * BM, 2 * w, lane);
+        a1 = dma_src<AKC>(A, m0 + t * BM, 2 * w + 1, lane);
+        sb0 = b0;
+        sb1 = b1;
+      },
+      ring, acc, tid, [&](int t, Acc& a) { epi(t, m0 + t * BM, a); });
 }
 
 // Full-K product of one output tile on the direct-to-LDS ring.
@@ -414,7 +433,8 @@ __device__ __forceinline__ void gemm_tile_dma(const Operand& A, const Operand& B
   __shared__ __attribute__((aligned(16))) bf16 s1[DMA ? 2 * kDmaOpElems : 8];               \
   __shared__ __attribute__((aligned(16))) bf16 s2[DMA ? 2 * kDmaOpElems : 8];               \
   __shared__ __attribute__((aligned(16))) bf16 s3[DMA ? 2 * kDmaOpElems : 8];               \
-  const DmaRing ring{{s0, s1, s2, s3}}
+  __shared__ __attribute__((aligned(16))) bf16 s4[DMA && kDmaStages > 4 ? 2 * kDmaOpElems : 8]; \
+  const DmaRing ring{{s0, s1, s2, s3, s4}}
 
 // XCD-aware tile order of a grouped GEMM: workgroups are dealt to the 8 XCDs
 // round-robin by index, so the tiles_n output tiles that share one row block

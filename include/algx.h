@@ -332,11 +332,15 @@ int32_t algx_ns_normalize(const float* x, void* out, int64_t K, int64_t MN, int3
  * A[m*lda + k] when a_kc (k-contiguous) else A[k*lda + m]; opB(n, k)
  * likewise with ldb and b_kc. C and D (optional: null skips beta) are
  * row-major [M][N] with ldc / ldd; D may be C. bf16 throughout; M, N, K,
- * leading dimensions and strides multiples of 8, pointers 16-byte aligned. */
+ * leading dimensions and strides multiples of 8, pointers 16-byte aligned.
+ * symmetric != 0 states that C is symmetric (M == N; the product symmetric,
+ * D symmetric when given), as X X^T and A A are: only the tiles on and above
+ * the diagonal are formed and mirrored. */
 int32_t algx_gemm_bf16_batched(const void* A, const void* B, const void* D, void* C,
                                int32_t batch, int32_t M, int32_t N, int32_t K, int32_t a_kc,
-                               int32_t b_kc, int64_t lda, int64_t ldb, int64_t ldd, int64_t ldc,
-                               int64_t stride_a, int64_t stride_b, int64_t stride_d,
+                               int32_t b_kc, int32_t symmetric, int64_t lda, int64_t ldb,
+                               int64_t ldd, int64_t ldc, int64_t stride_a, int64_t stride_b,
+                               int64_t stride_d,
                                int64_t stride_c, float alpha, float beta, void* stream);
 
 #ifdef __cplusplus

@@ -78,3 +78,31 @@ def test_newton_schulz_products_match_torch_iteration():
         Y = torch.baddbmm(Y, torch.bmm(Y, Y.transpose(1, 2).contiguous()), Y, beta=1.5, alpha=-0.5)
     rel = ((got.float() - Y.float()).norm() / Y.float().norm()).item()
     assert rel <= 2e-2, rel
+
+
+@pytest.mark.parametrize("batch,M,K", [(3, 520, 96), (8, 1024, 256), (2, 264, 72)])
+def test_batched_gemm_symmetric_products(batch, M, K):
+    """symmetric=True forms only the tiles on and above the diagonal and
+    mirrors them: X X^T (ragged tile counts; K = 72 takes the full schedule)
+    and c A A + b A with A symmetric."""
+    g = torch.Generator(device=DEV).manual_seed(M + K)
+    X = torch.randn((batch, M, K), generator=g, device=DEV).bfloat16()
+    A = O.gemm_bf16_batched(X, X, a_kc=True, b_kc=True, symmetric=True)
+    _check(A, _ref(X, X, True, True, None, 1.0, 0.0))
+    if K % 32 == 0:
+        # off-diagonal 256 x 256 blocks are exact mirrors
+        for i in range(0, M, 256):
+            for j in range(i + 256, M, 256):
+                assert torch.equal(A[:, j:j + 256, i:i + 256], A[:, i:i + 256, j:j + 256].transpose(1, 2))
+    As = ((A.float() + A.float().transpose(1, 2)) * 0.5).bfloat16()
+    Bm = O.gemm_bf16_batched(As, As, a_kc=True, b_kc=False, D=As, alpha=2.0315, beta=-4.775,
+                             symmetric=True)
+    _check(Bm, _ref(As, As, True, False, As, 2.0315, -4.775))
+
+
+def test_batched_gemm_symmetric_needs_square():
+    A = torch.zeros((2, 16, 32), device=DEV, dtype=torch.bfloat16)
+    B = torch.zeros((2, 24, 32), device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="M == N"):
+        O.gemm_bf16_batched(A, B, a_kc=True, b_kc=True, symmetric=True)
+
