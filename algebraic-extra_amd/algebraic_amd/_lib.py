@@ -25,7 +25,7 @@ class AttnVariant(ctypes.Structure):
     """algx_attn_variant (include/algx.h)."""
     _fields_ = [("kind", _i32), ("n", _i32), ("shift", _i32), ("fast_rho", _i32),
                 ("inv_stat", _i32), ("bounded_scores", _i32), ("precise_output", _i32),
-                ("clamp", _f32)]
+                ("clamp", _f32), ("poly_rho", _i32)]
 
 
 _VP = ctypes.POINTER(AttnVariant)

@@ -18,7 +18,10 @@ gfx950 HIP kernels of libalgx.so (include/algx.h).
 The TPU schedule flags (block sizes, resident/diagonal/head-resident
 backends, compact statistics) are validated exactly as the reference does but
 select nothing here: one MFMA schedule serves every case. ``poly_rho`` (the
-reference's opt-in polynomial radical) is not provided.
+reference's opt-in bounded radical, radical.py:26-38) evaluates rho and its
+slope by the reference's degree-4 polynomials where |x| <= 1 and exactly
+elsewhere; the reference makes that choice once per Pallas score tile, the
+kernels here per score (the two agree to ~3e-5 relative).
 """
 
 import math
@@ -94,7 +97,7 @@ def _c_variant(var: Variant) -> _lib.AttnVariant:
         kind=_lib.SOFTMAX if var.kind == "softmax" else _lib.ASINH, n=int(var.n),
         shift=int(var.shift), fast_rho=int(var.fast_rho), inv_stat=int(var.inv_stat),
         bounded_scores=int(var.bounded_scores), precise_output=int(var.precise_output),
-        clamp=float(var.clamp))
+        clamp=float(var.clamp), poly_rho=int(var.poly_rho))
 
 
 class _Plan(NamedTuple):
@@ -196,9 +199,6 @@ def flash_attention(q, k, v, sink_logit: Optional[torch.Tensor] = None, *, kind:
     if head_resident is True and not head_supported:
         raise ValueError("whole-head residency needs resident bfloat16 T=2048,D=64, "
                          "512-square public tiles, and compact statistics")
-    if poly_rho:
-        raise NotImplementedError("poly_rho (the TPU polynomial radical experiment) is not "
-                                  "provided by the MI355X kernels")
     if q.dtype not in (torch.bfloat16, torch.float32) or not (q.dtype == k.dtype == v.dtype):
         raise ValueError("flash_attention needs q, k, v of one dtype, bfloat16 or float32")
     if k.shape != q.shape or v.shape != q.shape:
@@ -214,6 +214,8 @@ def flash_attention(q, k, v, sink_logit: Optional[torch.Tensor] = None, *, kind:
     else:
         sink = None
     if range_guard and kind == "asinh" and n <= 32:
+        if poly_rho:
+            raise ValueError("range_guard is for exact radical evaluation")  # flash.py:835-836
         bound = min(16.0, var.clamp / 2)
         vmax = min(1e8, 1e37 / ((T + int(has_sink)) * (2 * bound + 1) ** n))
         low = var._replace(shift=False, inv_stat=True, bounded_scores=True)

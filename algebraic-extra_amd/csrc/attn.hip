@@ -30,6 +30,9 @@ int32_t to_kvar(const algx_attn_variant* v, KVariant& out, const char* which) {
   out.precise = v->precise_output != 0;
   out.clamp = v->clamp;
   out.slope = v->kind == ALGX_ASINH ? (float)v->n : 1.0f;
+  out.poly = v->kind == ALGX_ASINH && v->poly_rho != 0;
+  if (out.poly && (out.shift || v->n != 16))
+    return fail("attn: bounded radical approximation requires shift=False and n=16");
   return 0;
 }
 

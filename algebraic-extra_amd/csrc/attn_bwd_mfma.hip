@@ -45,7 +45,7 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 // p = rho^n * st: the statistic itself when it is 1/Z (inv_stat), its n-th
 // power otherwise ((rho * Z^(-1/n))^n = rho^n / Z, rho being clamped so rho^n
 // is finite).
-template <int MODE, bool FAST, bool BOUNDED, int L2N>
+template <int MODE, bool FAST, bool BOUNDED, int L2N, bool POLY>
 __device__ __forceinline__ void tile_grad(float s, float dpp, float st, float clamp, int log2n,
                                           float& p, float& ds) {
   if (MODE == MODE_SOFTMAX) {
@@ -55,7 +55,7 @@ __device__ __forceinline__ void tile_grad(float s, float dpp, float st, float cl
   }
   const float x = (MODE == MODE_NOSHIFT && !BOUNDED) ? __builtin_fminf(s, clamp) : s;
   float r;
-  const float rh = FAST ? rho_fast(x, r) : rho_exact(x, r);
+  const float rh = POLY ? rho_poly(x, r) : FAST ? rho_fast(x, r) : rho_exact(x, r);
   p = MODE == MODE_NOSHIFT ? powN<L2N>(rh, log2n) * st : powN<L2N>(rh * st, log2n);
   ds = (p * r) * dpp;
   if (MODE == MODE_NOSHIFT && !BOUNDED && !(s < clamp)) ds = 0.0f;
@@ -70,7 +70,7 @@ struct BwdLds {
   bf16 kt[HD * KTR];        // K^T of the workgroup [d][key]
 };
 
-template <int MODE, bool FAST, bool BOUNDED, int L2N>
+template <int MODE, bool FAST, bool BOUNDED, int L2N, bool POLY>
 __device__ __forceinline__ void bwd_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ stat, const float* __restrict__ di, const bf16* __restrict__ dout,
@@ -179,7 +179,7 @@ __device__ __forceinline__ void bwd_body(
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * j + i;
         float p, ds;
-        tile_grad<MODE, FAST, BOUNDED, L2N>(s[r], dp[r], st4[i], clamp, log2n, p, ds);
+        tile_grad<MODE, FAST, BOUNDED, L2N, POLY>(s[r], dp[r], st4[i], clamp, log2n, p, ds);
         if (DIAG && q0 + qo + i < kcol) {
           p = 0.0f;
           ds = 0.0f;
@@ -334,11 +334,11 @@ __global__ __launch_bounds__(NTHR, 1) void bwd_mfma_kernel(
     KVariant lo, KVariant hi, const int32_t* __restrict__ guard) {
   __shared__ __attribute__((aligned(16))) BwdLds lds;
   if (LO == HI || guard_in_range(guard))
-    bwd_body<LO & 3, (LO & 4) != 0, (LO & 8) != 0, (LO >> 4)>(q, k, v, stat, di, dout, dq_acc, dk,
-                                                              dv, T_, lo, lds);
+    bwd_body<cfg_mode(LO), cfg_fast(LO), cfg_bounded(LO), cfg_l2n(LO), cfg_poly(LO)>(
+        q, k, v, stat, di, dout, dq_acc, dk, dv, T_, lo, lds);
   else
-    bwd_body<HI & 3, (HI & 4) != 0, (HI & 8) != 0, (HI >> 4)>(q, k, v, stat, di, dout, dq_acc, dk,
-                                                              dv, T_, hi, lds);
+    bwd_body<cfg_mode(HI), cfg_fast(HI), cfg_bounded(HI), cfg_l2n(HI), cfg_poly(HI)>(
+        q, k, v, stat, di, dout, dq_acc, dk, dv, T_, hi, lds);
 }
 
 typedef void (*BwdFn)(const bf16*, const bf16*, const bf16*, const float*, const float*,

@@ -17,7 +17,13 @@ struct KVariant {
   int precise;   // write float32 output too
   float clamp;
   float slope;   // n for asinh, 1 for softmax (flash.py:430, :441)
+  int poly;      // bounded radical (radical.py:26-38)
 };
+
+// rho and its slope factor r of the variant (flash.py:91-92).
+__device__ __forceinline__ float rho_of(const KVariant& v, float x, float& r) {
+  return v.poly ? rho_poly(x, r) : rho_var(x, v.fast, r);
+}
 
 constexpr float kNeg = -1e4f;           // flash.py:55
 constexpr float kLog2e = 1.4426950408889634f;
@@ -38,7 +44,7 @@ __device__ __forceinline__ float bwd_weight(const KVariant& v, float s, float st
     keep = s < v.clamp;
   }
   float r;
-  float rh = rho_var(x, v.fast, r);
+  float rh = rho_of(v, x, r);
   rr = r;
   return v.inv_stat ? pow2n(rh, v.log2n) * stat : pow2n(rh * stat, v.log2n);
 }
@@ -51,7 +57,7 @@ __device__ __forceinline__ void sink_init(const KVariant& v, bool has_sink, floa
     if (has_sink) {
       float x = v.bounded ? b : __builtin_fminf(b, v.clamp);
       float r;
-      l = pow2n(rho_var(x, v.fast, r), v.log2n);
+      l = pow2n(rho_of(v, x, r), v.log2n);
     } else {
       l = 0.0f;
     }
@@ -76,7 +82,7 @@ __device__ __forceinline__ float sink_grad_term(const KVariant& v, float b, floa
   const bool clipped = !v.shift && !v.bounded;
   const float bb = clipped ? __builtin_fminf(b, v.clamp) : b;
   float r;
-  const float rh = rho_exact(bb, r);
+  const float rh = v.poly ? rho_poly(bb, r) : rho_exact(bb, r);
   const float mass = v.inv_stat ? pow2n(rh, v.log2n) * stat : pow2n(rh * stat, v.log2n);
   float slope = v.slope * r;
   if (clipped && !(b < v.clamp)) slope = 0.0f;

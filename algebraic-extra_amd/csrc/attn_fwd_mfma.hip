@@ -24,7 +24,7 @@ namespace algx {
 namespace mfma {
 namespace {
 
-template <int MODE, bool FAST, bool BOUNDED, int L2N>
+template <int MODE, bool FAST, bool BOUNDED, int L2N, bool POLY>
 __device__ __forceinline__ void fwd_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
@@ -181,7 +181,8 @@ __device__ __forceinline__ void fwd_body(
           const float s = cur[mt][r];
           const float x = BOUNDED ? s : __builtin_fminf(s, var.clamp);
           float rr;
-          float p = powN<L2N>(FAST ? rho_fast(x, rr) : rho_exact(x, rr), log2n);
+          float p = powN<L2N>(POLY ? rho_poly(x, rr) : FAST ? rho_fast(x, rr) : rho_exact(x, rr),
+                              log2n);
           if (DIAG && k0 + 32 * mt + 8 * (r >> 2) + 4 * g + (r & 3) > qrow) p = 0.0f;
           cur[mt][r] = p;
           lsum += p;
@@ -335,10 +336,10 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
   __shared__ __attribute__((aligned(16))) bf16 Vs[2][FBN * VSTR];
   __shared__ float red[3][4];
   if (LO == HI || guard_in_range(guard))
-    fwd_body<LO & 3, (LO & 4) != 0, (LO & 8) != 0, (LO >> 4)>(
+    fwd_body<cfg_mode(LO), cfg_fast(LO), cfg_bounded(LO), cfg_l2n(LO), cfg_poly(LO)>(
         q, k, v, sink, o, o_precise, stat, H, T_, lo, prep, Ks, Vs, red, blockIdx.x, gridDim.x);
   else
-    fwd_body<HI & 3, (HI & 4) != 0, (HI & 8) != 0, (HI >> 4)>(
+    fwd_body<cfg_mode(HI), cfg_fast(HI), cfg_bounded(HI), cfg_l2n(HI), cfg_poly(HI)>(
         q, k, v, sink, o, o_precise, stat, H, T_, hi, prep, Ks, Vs, red, blockIdx.x, gridDim.x);
 }
 
@@ -399,7 +400,7 @@ __global__ __launch_bounds__(256, 2) void fwd_fallback_kernel(
   if (ok) return;
   for (int b = blockIdx.x; b < ntiles; b += gridDim.x) {
     __syncthreads();  // LDS of the previous tile is no longer read
-    fwd_body<HI & 3, (HI & 4) != 0, (HI & 8) != 0, (HI >> 4)>(
+    fwd_body<cfg_mode(HI), cfg_fast(HI), cfg_bounded(HI), cfg_l2n(HI), cfg_poly(HI)>(
         q_s, k, v, sink, o, o_precise, stat, H, T_, hi, FwdPrep{}, Ks, Vs, red, b, ntiles);
   }
 }

@@ -65,7 +65,7 @@ __global__ __launch_bounds__(kTile) void fwd_generic_kernel(
       for (int jj = 0; jj <= jmax; ++jj) {
         const float x = var.bounded ? s[jj] : __builtin_fminf(s[jj], var.clamp);
         float r;
-        const float p = pow2n(rho_var(x, var.fast, r), var.log2n);
+        const float p = pow2n(rho_of(var, x, r), var.log2n);
         l += p;
         const float pb = round_to<T>(p);
 #pragma unroll

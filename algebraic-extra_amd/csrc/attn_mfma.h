@@ -27,14 +27,21 @@ struct FwdPrep {
 // (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4], lgkmcnt[11:8]).
 constexpr int kWaitVm0 = 0x0F70;
 
-// Kernel configuration packed in one int: MODE | FAST << 2 | BOUNDED << 3 | L2N << 4.
-constexpr int cfg_of(int mode, bool fast, bool bounded, int l2n) {
-  return mode | (fast ? 4 : 0) | (bounded ? 8 : 0) | (l2n << 4);
+// Kernel configuration packed in one int:
+// MODE | FAST << 2 | BOUNDED << 3 | L2N << 4 (3 bits) | POLY << 7.
+constexpr int cfg_of(int mode, bool fast, bool bounded, int l2n, bool poly = false) {
+  return mode | (fast ? 4 : 0) | (bounded ? 8 : 0) | (l2n << 4) | (poly ? 128 : 0);
 }
+constexpr int cfg_mode(int c) { return c & 3; }
+constexpr bool cfg_fast(int c) { return (c & 4) != 0; }
+constexpr bool cfg_bounded(int c) { return (c & 8) != 0; }
+constexpr int cfg_l2n(int c) { return (c >> 4) & 7; }
+constexpr bool cfg_poly(int c) { return (c & 128) != 0; }
 // Power template argument: n = 8, 16, 32 unrolled; other n by a runtime loop.
 inline int l2n_arg(int log2n) { return (log2n >= 3 && log2n <= 5) ? log2n : 0; }
 inline int cfg_for(const KVariant& v) {
   if (v.kind == ALGX_SOFTMAX) return cfg_of(MODE_SOFTMAX, false, false, 1);
+  if (v.poly) return cfg_of(MODE_NOSHIFT, false, v.bounded != 0, l2n_arg(v.log2n), true);
   if (v.shift) return cfg_of(MODE_SHIFT, v.fast != 0, false, l2n_arg(v.log2n));
   return cfg_of(MODE_NOSHIFT, v.fast != 0, v.bounded != 0, l2n_arg(v.log2n));
 }
@@ -120,7 +127,8 @@ template <int L2N> __device__ __forceinline__ float powN(float x, int log2n) {
   X(K, cfg_of(MODE_NOSHIFT, true, false, 3)) X(K, cfg_of(MODE_NOSHIFT, true, false, 4)) \
   X(K, cfg_of(MODE_NOSHIFT, true, false, 5)) X(K, cfg_of(MODE_NOSHIFT, true, false, 0)) \
   X(K, cfg_of(MODE_NOSHIFT, false, false, 3)) X(K, cfg_of(MODE_NOSHIFT, false, false, 4)) \
-  X(K, cfg_of(MODE_NOSHIFT, false, false, 5)) X(K, cfg_of(MODE_NOSHIFT, false, false, 0))
+  X(K, cfg_of(MODE_NOSHIFT, false, false, 5)) X(K, cfg_of(MODE_NOSHIFT, false, false, 0)) \
+  X(K, cfg_of(MODE_NOSHIFT, false, false, 4, true))
 
 #define ALGX_PICK_SINGLE(K, C) \
   if (cl == (C)) return K<(C), (C)>;

@@ -72,6 +72,29 @@ __device__ __forceinline__ float rho_exact(float x, float& r) {
 __device__ __forceinline__ float rho_var(float x, bool fast, float& r) {
   return fast ? rho_fast(x, r) : rho_exact(x, r);
 }
+// Bounded radical (radical.py:13-38): on |x| <= 1, x + sqrt(1+t) and
+// r = 1/sqrt(1+t) as degree-4 polynomials in t = x^2 (Horner, the
+// reference's float32 coefficients); outside, the stable exact radical. The
+// reference picks the polynomial for a whole score tile whose max |x| is at
+// most 1; here each score picks it for itself.
+__device__ __forceinline__ float rho_poly(float x, float& r) {
+  if (__builtin_fabsf(x) <= 1.0f) {
+    const float t = x * x;
+    float s = -.010264432643176741f;
+    s = __builtin_fmaf(s, t, .04451694257534509f);
+    s = __builtin_fmaf(s, t, -.11935047485233699f);
+    s = __builtin_fmaf(s, t, .49927168521732207f);
+    s = __builtin_fmaf(s, t, 1.0000227161113386f);
+    float q = .05025262090029994f;
+    q = __builtin_fmaf(q, t, -.1841886600636537f);
+    q = __builtin_fmaf(q, t, .3364554110926816f);
+    q = __builtin_fmaf(q, t, -.49515903732516475f);
+    q = __builtin_fmaf(q, t, .9998514827226793f);
+    r = q;
+    return x + s;
+  }
+  return rho_exact(x, r);
+}
 // x^(2^log2n) by repeated squaring == int_pow for powers of two (flash.py:95-104).
 __device__ __forceinline__ float pow2n(float x, int log2n) {
   for (int i = 0; i < log2n; ++i) x = x * x;

@@ -41,6 +41,8 @@ typedef struct {
   int32_t bounded_scores;  /* guard passed: no clamp of scores                 */
   int32_t precise_output;  /* also write the float32 output (o_precise)        */
   float clamp;             /* score clamp when !shift && !bounded_scores       */
+  int32_t poly_rho;        /* bounded radical (radical.py:26-38): polynomial   *
+                            * on |x| <= 1; asinh, shift=False, n = 16 only     */
 } algx_attn_variant;
 
 /* Text of the last error on this thread ("" when none). */

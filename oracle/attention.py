@@ -27,7 +27,7 @@ from typing import NamedTuple, Optional
 
 import numpy as np
 
-from .common import F64, cast, inv_root, ipow, rho, rho_exact, root
+from .common import F64, bounded_radical, cast, inv_root, ipow, rho, rho_exact, root, tiled_rho
 
 NEG = -1e4  # flash.py:55 -- finite "minus infinity" of the shifted kernels
 
@@ -115,7 +115,7 @@ def _scores(qs, k):
     return np.einsum("bhqd,bhkd->bhqk", np.asarray(qs, F64), np.asarray(k, F64))
 
 
-def forward(qs, k, v, sink, var, has_sink, dtype):
+def forward(qs, k, v, sink, var, has_sink, dtype, block=(512, 512)):
     """Kernel forward on pre-scaled ``qs``; returns ``(o, o_residual, stat)``.
 
     ``sink`` is the (H,) kernel-unit sink (already divided by ``c``).
@@ -144,11 +144,15 @@ def forward(qs, k, v, sink, var, has_sink, dtype):
         stat = m + np.log(l)
     elif not var.shift:
         x = s if var.bounded_scores else np.minimum(s, var.clamp)
-        p = np.where(mask, ipow(rho(x, var.fast_rho)[0], var.n), 0.0)
+        bq, bk = min(block[0], T), min(block[1], T)
+        p = np.where(mask, ipow(tiled_rho(x, var.fast_rho, var.poly_rho, bq, bk)[0], var.n), 0.0)
         l = p.sum(-1)
         if has_sink:
             xb = b if var.bounded_scores else np.minimum(b, var.clamp)
-            l = l + ipow(rho(xb, var.fast_rho)[0], var.n)
+            # one head's sink fills the l_sc tile (flash.py:201-205)
+            rb = (np.stack([bounded_radical(xb[:, h])[0] for h in range(H)], axis=1)
+                  if var.poly_rho else rho(xb, var.fast_rho)[0])
+            l = l + ipow(rb, var.n)
         stat = 1.0 / l if var.inv_stat else inv_root(l, var.n)
     else:
         m = np.max(np.where(mask, s, -np.inf), axis=-1)
@@ -174,7 +178,7 @@ def sink_mass_and_slope(sink, stat, var):
     if var.kind == "softmax":
         return np.exp(sink[None, :, None] - stat), np.ones_like(sink)
     bb = np.minimum(sink, var.clamp) if (not var.shift and not var.bounded_scores) else sink
-    rh, r = rho_exact(bb)
+    rh, r = bounded_radical(bb) if var.poly_rho else rho_exact(bb)   # over all heads at once
     mass = (ipow(rh[None, :, None], var.n) * stat if var.inv_stat
             else ipow(rh[None, :, None] * stat, var.n))
     slope = var.n * r
@@ -183,7 +187,7 @@ def sink_mass_and_slope(sink, stat, var):
     return mass, slope
 
 
-def backward(qs, k, v, sink, o_res, stat, do, var, has_sink, dtype):
+def backward(qs, k, v, sink, o_res, stat, do, var, has_sink, dtype, block=(512, 512)):
     """Kernel VJP w.r.t. (qs, k, v, sink); flash.py:333-361, :630-638, :718-726.
 
     ``dq`` is w.r.t. the pre-scaled query (the wrapper applies ``scale``).
@@ -202,7 +206,8 @@ def backward(qs, k, v, sink, o_res, stat, do, var, has_sink, dtype):
             x = s if var.bounded_scores else np.minimum(s, var.clamp)
         else:
             x = np.where(mask, s, 0.0)
-        rh, r = rho(x, var.fast_rho)
+        bq, bk = min(block[0], T), min(block[1], T)
+        rh, r = tiled_rho(x, var.fast_rho, var.poly_rho, bq, bk)
         p = ipow(rh, var.n) * stat_ if var.inv_stat else ipow(rh * stat_, var.n)
     p = np.where(mask, p, 0.0)
     dp = np.einsum("bhqd,bhkd->bhqk", do, np.asarray(v, F64))
@@ -235,7 +240,8 @@ class Result(NamedTuple):
 
 def flash_attention(q, k, v, sink_logit=None, *, kind="softmax", n=16, c=16.0,
                     shift=None, fast_rho=None, inv_stat=None, compact_stat=True,
-                    poly_rho=False, range_guard=False, dtype="f32", do=None):
+                    poly_rho=False, range_guard=False, dtype="f32", do=None, block=512,
+                    block_q=None, block_k=None):
     """Public wrapper semantics, flash.py:793-857, plus its custom VJP.
 
     Inputs are float64 arrays holding values representable in ``dtype``
@@ -244,9 +250,10 @@ def flash_attention(q, k, v, sink_logit=None, *, kind="softmax", n=16, c=16.0,
     """
     q, k, v = (np.asarray(a, F64) for a in (q, k, v))
     B, H, T, D = q.shape
+    tiles = (block_q or block, block_k or block)   # Pallas score tiles (poly_rho's cond)
     var = make_variant(kind, n, c, T, shift, fast_rho, inv_stat, compact_stat, poly_rho)
-    if poly_rho:
-        raise NotImplementedError("poly_rho is not restated by the oracle")
+    if poly_rho and range_guard and kind == "asinh" and n <= 32:
+        raise ValueError("range_guard is for exact radical evaluation")   # flash.py:835-836
     unit = 1.0 if kind == "softmax" else float(c)
     scale = 1.0 / (math.sqrt(D) * unit)
     has_sink = sink_logit is not None
@@ -262,10 +269,11 @@ def flash_attention(q, k, v, sink_logit=None, *, kind="softmax", n=16, c=16.0,
         in_range = guard_in_range(qs, k, v, sink, var, has_sink)
         low, high = low_high(var)
         var = low if in_range else high
-    o, o_res, stat = forward(qs, k, v, sink, var, has_sink, dtype)
+    o, o_res, stat = forward(qs, k, v, sink, var, has_sink, dtype, tiles)
     grads = None
     if do is not None:
-        dq_s, dk, dv, dsink, _ = backward(qs, k, v, sink, o_res, stat, do, var, has_sink, dtype)
+        dq_s, dk, dv, dsink, _ = backward(qs, k, v, sink, o_res, stat, do, var, has_sink, dtype,
+                                          tiles)
         dq = cast(cast(dq_s, "f32") * scale, dtype)               # VJP of flash.py:833
         if has_sink:
             d_in = dsink / unit                                    # VJP of flash.py:828

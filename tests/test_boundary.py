@@ -36,7 +36,7 @@ def test_library_loads_and_exports_every_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.algx_version() == 1
+    assert lib.algx_version() == 2
     assert lib.algx_last_error() == b""
 
 
@@ -97,8 +97,11 @@ def test_flash_validation_mirrors_reference():
         flash_attention(x, x, x, kind="asinh", n=12)
     with pytest.raises(ValueError, match="unknown attention kernel"):
         flash_attention(x, x, x, kind="relu")
-    with pytest.raises(NotImplementedError, match="poly_rho"):
-        flash_attention(x, x, x, kind="asinh", n=16, shift=False, poly_rho=True)
+    # poly_rho (flash.py:757-758, :835-836)
+    with pytest.raises(ValueError, match="shift=False and n=16"):
+        flash_attention(x, x, x, kind="asinh", n=8, shift=False, poly_rho=True)
+    with pytest.raises(ValueError, match="range_guard is for exact radical"):
+        flash_attention(x, x, x, kind="asinh", n=16, shift=False, poly_rho=True, range_guard=True)
 
 
 def test_make_variant_matches_reference_defaults():

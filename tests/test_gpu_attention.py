@@ -188,6 +188,47 @@ def test_whole_head_model_shape(mode):
         assert_bf16(a, b, what=f"{mode}:{nm}")
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("blocks", [(128, 128), (128, 256), (256, 128)])
+def test_model_attention_polynomial_radical(dtype, blocks):
+    """test_flash_kernel_tpu.py:69-97, mode "polynomial": poly_rho (the
+    bounded radical, radical.py:26-38) at n=16, c=8 with a sink against the
+    exact functions with the reference's tolerances; and against the oracle's
+    restatement of the reference's per-tile choice, within the polynomial's
+    approximation error (the kernels choose per score)."""
+    shape = (1, 2, 512, 64)
+    q, k, v, g = _rand(shape, 13, dtype=dtype)
+    sink = torch.from_numpy(np.random.default_rng(14).standard_normal((1, 2, 1, 1)).astype(np.float32))
+    kw = dict(kind="asinh", n=16, c=8.0, shift=False, fast_rho=True, inv_stat=True)
+    bq, bk = blocks
+    got = _run(q, k, v, g, sink, block_q=bq, block_k=bk, poly_rho=True, **kw)
+    dense = OA.dense_asinh_attention(to_np(q), to_np(k), to_np(v), n=16, c=8.0, sink_logit=to_np(sink),
+                                     p_dtype=dtype)
+    np.testing.assert_allclose(got[0], dense, atol=0.012, rtol=0.012)
+    exact, _ = _oracle(q, k, v, g, sink, dtype, kind="asinh", n=16, c=8.0, shift=False,
+                       fast_rho=False, inv_stat=True)
+    for a, b in zip(got[1:], exact[1:]):
+        assert rel_l2(a, b) < (0.02 if dtype == "bf16" else 0.005)
+    poly, _ = _oracle(q, k, v, g, sink, dtype, poly_rho=True, block_q=bq, block_k=bk, **kw)
+    for a, b, nm in zip(got, poly, ("o", "dq", "dk", "dv", "dsink")):
+        if dtype == "f32":
+            # weights differ by at most the polynomial's error (~7e-4 at n=16)
+            assert rel_l2(a, b) <= 2e-3, (nm, rel_l2(a, b))
+        elif nm == "dsink":
+            assert rel_l2(a, b) <= 1e-2, (nm, rel_l2(a, b))
+        else:
+            assert_dtype_close(a, b, dtype, what=nm)
+
+
+def test_polynomial_radical_refuses_guard_and_shift():
+    q = torch.zeros((1, 1, 64, 64), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="range_guard"):
+        flash_attention(q, q, q, kind="asinh", n=16, c=8.0, poly_rho=True, range_guard=True,
+                        shift=False)
+    with pytest.raises(ValueError, match="shift=False and n=16"):
+        flash_attention(q, q, q, kind="asinh", n=16, c=8.0, poly_rho=True, shift=True)
+
+
 def test_mfma_path_matches_generic_kernels():
     """The MFMA kernels and the scalar kernels agree on every output (bf16, T=512)."""
     shape = (2, 4, 512, 64)

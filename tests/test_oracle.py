@@ -18,7 +18,8 @@ import torch
 from oracle import attention as OA
 from oracle import head as OH
 from oracle import qknorm as OQ
-from oracle.common import inv_root, ipow, rho_exact, rho_fast, root, to_bf16
+from oracle.common import (bounded_radical, inv_root, ipow, rho_exact, rho_fast, root, tiled_rho,
+                           to_bf16)
 
 # ---------------------------------------------------------------------------
 # elementwise algebra
@@ -46,6 +47,35 @@ def test_rho_known_answers():
     assert np.isfinite(v) and v > 0
     assert math.isclose(float(v), 1.0 / (1e6 + math.sqrt(1.0 + 1e12)), rel_tol=1e-3)
     assert rho_exact(np.float32(1e6))[0] > 1e6
+
+
+def test_bounded_radical_pins():
+    """radical.py:13-38. On |x| <= 1 the polynomials approximate rho(x) and
+    r = 1/sqrt(1+x^2) (the fit's error: < 5e-5 and < 2e-4 relative); at x = 0
+    they give their constant terms (coefficient order); any |x| > 1 in the
+    array sends all of it down the exact stable radical (one cond per call)."""
+    x = np.linspace(-1.0, 1.0, 4001)
+    rp, rr = bounded_radical(x)
+    re, ri = rho_exact(x)
+    assert np.max(np.abs(rp - re) / re) < 5e-5
+    assert np.max(np.abs(rr - ri) / ri) < 2e-4
+    r0, s0 = bounded_radical(np.zeros(3))
+    assert np.allclose(r0, np.float32(1.0000227161113386)) and np.allclose(s0, np.float32(.9998514827226793))
+    # the sqrt(1+t) fit at t = 1 is sqrt(2), the rsqrt fit 1/sqrt(2) (both to the fit error)
+    assert abs(bounded_radical(np.array([1.0]))[0][0] - (1 + math.sqrt(2))) < 1e-4
+    mixed = np.array([0.25, -0.5, 1.5])
+    np.testing.assert_array_equal(bounded_radical(mixed)[0], rho_exact(mixed)[0])
+    # per (head, tile): one large score makes only its own tile of its own head exact
+    xs = np.full((1, 2, 4, 4), 0.3)
+    xs[0, 1, 0, 3] = 2.0
+    rh, _ = tiled_rho(xs, True, True, 2, 2)
+    poly_val = bounded_radical(np.array([0.3]))[0][0]
+    exact_val = rho_exact(np.array([0.3]))[0][0]
+    assert poly_val != exact_val
+    np.testing.assert_array_equal(rh[0, 0], poly_val)
+    np.testing.assert_array_equal(rh[0, 1, 0:2, 2:4][rh[0, 1, 0:2, 2:4] < 1.5], exact_val)
+    np.testing.assert_array_equal(rh[0, 1, 2:4], poly_val)
+    np.testing.assert_array_equal(rh[0, 1, 0:2, 0:2], poly_val)
 
 
 def test_ipow_and_roots():
