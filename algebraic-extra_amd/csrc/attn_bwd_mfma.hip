@@ -295,13 +295,18 @@ __device__ __forceinline__ void bwd_body(
     const int q0 = qt * BQ;
     f32x16 s0, dp0, s1, dp1;
     bf16x8 pb0[2], db0[2], pb1[2], db1[2];
+    // Waves w and w + 4 share a SIMD and the tile's barrier; the upper four
+    // form the previous tile's dQ first, so the pair's MFMA and VALU phases
+    // are offset rather than coincident.
+    const bool dq_first = w >= 4;
+    if (dq_first) dq_tile(qt - 1, buf ^ 1);
     half_scores(buf, 0, s0, dp0);
     half_grads(std::false_type{}, buf, q0, 0, s0, dp0, pb0, db0);
     half_scores(buf, 1, s1, dp1);
     half_update(buf, 0, pb0, db0);
     half_grads(std::false_type{}, buf, q0, 1, s1, dp1, pb1, db1);
     half_update(buf, 1, pb1, db1);
-    dq_tile(qt - 1, buf ^ 1);
+    if (!dq_first) dq_tile(qt - 1, buf ^ 1);
     lstore(buf ^ 1);
     gload(qt + 2 < nqt ? qt + 2 : nqt - 1);
     __syncthreads();
