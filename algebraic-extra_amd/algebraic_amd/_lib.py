@@ -30,6 +30,14 @@ class AttnVariant(ctypes.Structure):
 
 _VP = ctypes.POINTER(AttnVariant)
 
+
+class GemmBatch(ctypes.Structure):
+    """algx_gemm_batch (include/algx.h)."""
+    _fields_ = [("A", _p), ("B", _p), ("D", _p), ("C", _p), ("batch", _i32), ("M", _i32),
+                ("N", _i32), ("K", _i32), ("lda", _i64), ("ldb", _i64), ("ldd", _i64),
+                ("ldc", _i64), ("stride_a", _i64), ("stride_b", _i64), ("stride_d", _i64),
+                ("stride_c", _i64)]
+
 # name -> (restype, argtypes); must match include/algx.h.
 SIGNATURES = {
     "algx_last_error": (ctypes.c_char_p, []),
@@ -85,6 +93,8 @@ SIGNATURES = {
     "algx_gemm_bf16_batched": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                       _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                       _f32, _f32, _p]),
+    "algx_gemm_bf16_grouped": (_i32, [ctypes.POINTER(GemmBatch), _i32, _i32, _i32, _i32, _f32,
+                                      _f32, _p]),
     "algx_qk_prologue_fwd": (_i32, [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,
                                     _i32, _i32, _i32, _f32, _p]),
     "algx_qk_prologue_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32]),

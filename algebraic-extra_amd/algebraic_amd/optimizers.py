@@ -110,6 +110,28 @@ def _ns_wide(X: torch.Tensor, steps: int, eps: float, ns_dtype: torch.dtype) -> 
     return _ns_iterate(Xn, steps)
 
 
+def _gemm_problem(A, B, a_kc, b_kc, D, out, who):
+    """One batch of the GEMM core's products: checked shapes, the output
+    (allocated when not given) and its algx_gemm_batch descriptor."""
+    kb, ra, ca = A.shape
+    M, K = (ra, ca) if a_kc else (ca, ra)
+    N, Kb = (B.shape[1], B.shape[2]) if b_kc else (B.shape[2], B.shape[1])
+    if B.shape[0] != kb or Kb != K:
+        raise ValueError(f"{who}: shapes {tuple(A.shape)} and {tuple(B.shape)} do not chain")
+    for t in (A, B) + tuple(x for x in (D, out) if x is not None):
+        if t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{who}: operands must be contiguous bf16 device tensors")
+    for name, t in (("D", D), ("out", out)):
+        if t is not None and tuple(t.shape) != (kb, M, N):
+            raise ValueError(f"{who}: {name} must be (batch, M, N)")
+    if out is None:
+        out = torch.empty((kb, M, N), dtype=torch.bfloat16, device=A.device)
+    desc = _lib.GemmBatch(A.data_ptr(), B.data_ptr(), D.data_ptr() if D is not None else None,
+                          out.data_ptr(), kb, M, N, K, A.shape[2], B.shape[2], N, N, ra * ca,
+                          B.shape[1] * B.shape[2], M * N, M * N)
+    return desc, out
+
+
 def gemm_bf16_batched(A: torch.Tensor, B: torch.Tensor, *, a_kc: bool, b_kc: bool,
                       D: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0,
                       out: Optional[torch.Tensor] = None, symmetric: bool = False) -> torch.Tensor:
@@ -121,25 +143,34 @@ def gemm_bf16_batched(A: torch.Tensor, B: torch.Tensor, *, a_kc: bool, b_kc: boo
     B[i]^T. So C = A B^T for (True, True) and C = A B for (True, False).
     ``symmetric`` states that C is symmetric (the product and D): only the
     tiles on and above the diagonal are formed, then mirrored."""
-    kb, ra, ca = A.shape
-    M, K = (ra, ca) if a_kc else (ca, ra)
-    N, Kb = (B.shape[1], B.shape[2]) if b_kc else (B.shape[2], B.shape[1])
-    if B.shape[0] != kb or Kb != K:
-        raise ValueError(f"gemm_bf16_batched: shapes {tuple(A.shape)} and {tuple(B.shape)} "
-                         "do not chain")
-    for t in (A, B) + ((D,) if D is not None else ()):
-        if t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous():
-            raise ValueError("gemm_bf16_batched: operands must be contiguous bf16 device tensors")
-    if D is not None and tuple(D.shape) != (kb, M, N):
-        raise ValueError("gemm_bf16_batched: D must be (batch, M, N)")
-    if out is None:
-        out = torch.empty((kb, M, N), dtype=torch.bfloat16, device=A.device)
-    _lib.call("algx_gemm_bf16_batched", _lib.ptr(A), _lib.ptr(B),
-              _lib.ptr(D) if D is not None else None, _lib.ptr(out), kb, M, N, K,
-              int(a_kc), int(b_kc), int(symmetric), A.shape[2], B.shape[2], N, N, ra * ca,
-              B.shape[1] * B.shape[2],
-              M * N, M * N, float(alpha), float(beta if D is not None else 0.0), _lib.stream())
+    g, out = _gemm_problem(A, B, a_kc, b_kc, D, out, "gemm_bf16_batched")
+    _lib.call("algx_gemm_bf16_batched", g.A, g.B, g.D, g.C, g.batch, g.M, g.N, g.K,
+              int(a_kc), int(b_kc), int(symmetric), g.lda, g.ldb, g.ldd, g.ldc, g.stride_a,
+              g.stride_b, g.stride_d, g.stride_c, float(alpha),
+              float(beta if D is not None else 0.0), _lib.stream())
     return out
+
+
+def gemm_bf16_grouped(problems, *, a_kc: bool, b_kc: bool, alpha: float = 1.0,
+                      beta: float = 0.0, symmetric: bool = False):
+    """gemm_bf16_batched over up to four batches of different shapes in one
+    launch (algx_gemm_bf16_grouped): ``problems`` is a list of (A, B, D, out)
+    with D and out optional (None), the layouts, symmetry and coefficients
+    shared. Returns the outputs, equal bit for bit to one
+    gemm_bf16_batched call per batch."""
+    if len(problems) > 4:
+        raise ValueError("gemm_bf16_grouped: at most 4 batches per launch")
+    descs, outs = [], []
+    for A, B, D, out in problems:
+        g, out = _gemm_problem(A, B, a_kc, b_kc, D, out, "gemm_bf16_grouped")
+        if D is None and beta != 0.0:
+            raise ValueError("gemm_bf16_grouped: beta needs every batch's D")
+        descs.append(g)
+        outs.append(out)
+    arr = (_lib.GemmBatch * max(1, len(descs)))(*descs)
+    _lib.call("algx_gemm_bf16_grouped", arr, len(descs), int(a_kc), int(b_kc), int(symmetric),
+              float(alpha), float(beta), _lib.stream())
+    return outs
 
 
 def _ns_native_ok(X: torch.Tensor) -> bool:
@@ -149,40 +180,57 @@ def _ns_native_ok(X: torch.Tensor) -> bool:
 
 
 def _ns_iterate(X: torch.Tensor, steps: int) -> torch.Tensor:
-    """The iteration on a normalised, contiguous batch (k, m, n), m <= n.
+    """The iteration on a normalised, contiguous batch (k, m, n), m <= n."""
+    return _ns_iterate_many([X], steps)[0]
 
-    Each update is one batched GEMM with its linear combination folded into
-    the GEMM's own alpha/beta: B = b A + c A A and X <- a X + B X, and
+
+def _ns_iterate_many(Xs_in, steps: int):
+    """The iteration on normalised, contiguous batches (k, m, n), m <= n, of
+    any mix of shapes.
+
+    Each update is one GEMM with its linear combination folded into the
+    GEMM's own alpha/beta: B = b A + c A A and X <- a X + B X, and
     X <- 1.5 X - 0.5 (X X^T) X for the refinements. bf16 device batches run
-    on libalgx's GEMM core: X X^T reads X k-contiguous on both sides (no
-    transpose is formed), A A and B X read their second operand as [k][n],
-    and every product writes a buffer of its own (no self copy)."""
+    on libalgx's GEMM core, all batches of one product in one launch
+    (gemm_bf16_grouped, four at most): X X^T reads X k-contiguous on both
+    sides (no transpose is formed), A A and B X read their second operand as
+    [k][n], and every product writes a buffer of its own (no self copy)."""
     a, b, c = _NS_ABC
-    if _ns_native_ok(X):
-        k, m, n = X.shape
-        A = torch.empty((k, m, m), dtype=X.dtype, device=X.device)
-        Bm = torch.empty_like(A)
-        Xs = [X, torch.empty_like(X)]
-        cur = 0
+    if 0 < len(Xs_in) <= 4 and all(_ns_native_ok(X) for X in Xs_in):
+        st = []
+        for X in Xs_in:
+            k, m, n = X.shape
+            A = torch.empty((k, m, m), dtype=X.dtype, device=X.device)
+            st.append({"A": A, "B": torch.empty_like(A), "X": [X, torch.empty_like(X)]})
+        if all(t.data_ptr() % 16 == 0 for e in st for t in (e["A"], e["B"], e["X"][1])):
+            cur = 0
 
-        def update(coef_mat, acc_coef, own_coef):
-            # X <- own_coef X + acc_coef (coef_mat X), into the other buffer
-            nonlocal cur
-            gemm_bf16_batched(coef_mat, Xs[cur], a_kc=True, b_kc=False, D=Xs[cur],
-                              alpha=acc_coef, beta=own_coef, out=Xs[1 - cur])
-            cur = 1 - cur
+            def gram():
+                # A = X X^T: symmetric, upper-triangle tiles only
+                gemm_bf16_grouped([(e["X"][cur], e["X"][cur], None, e["A"]) for e in st],
+                                  a_kc=True, b_kc=True, symmetric=True)
 
-        if Xs[1].data_ptr() % 16 == 0 and A.data_ptr() % 16 == 0 and Bm.data_ptr() % 16 == 0:
-            # X X^T and b A + c A A are symmetric: upper-triangle tiles only
+            def update(mat, acc_coef, own_coef):
+                # X <- own_coef X + acc_coef (mat X), into the other buffer
+                nonlocal cur
+                gemm_bf16_grouped([(e[mat], e["X"][cur], e["X"][cur], e["X"][1 - cur])
+                                   for e in st], a_kc=True, b_kc=False, alpha=acc_coef,
+                                  beta=own_coef)
+                cur = 1 - cur
+
             for _ in range(steps):
-                gemm_bf16_batched(Xs[cur], Xs[cur], a_kc=True, b_kc=True, out=A, symmetric=True)
-                gemm_bf16_batched(A, A, a_kc=True, b_kc=False, D=A, alpha=c, beta=b, out=Bm,
-                                  symmetric=True)
-                update(Bm, 1.0, a)
+                gram()
+                # B = b A + c A A, symmetric as A is
+                gemm_bf16_grouped([(e["A"], e["A"], e["A"], e["B"]) for e in st], a_kc=True,
+                                  b_kc=False, alpha=c, beta=b, symmetric=True)
+                update("B", 1.0, a)
             for _ in range(2):
-                gemm_bf16_batched(Xs[cur], Xs[cur], a_kc=True, b_kc=True, out=A, symmetric=True)
-                update(A, -0.5, 1.5)
-            return Xs[cur]
+                gram()
+                update("A", -0.5, 1.5)
+            return [e["X"][cur] for e in st]
+    if len(Xs_in) > 1:
+        return [_ns_iterate_many([X], steps)[0] for X in Xs_in]
+    X = Xs_in[0]
 
     def gram(x):
         return torch.bmm(x, _mT(x))
@@ -193,7 +241,7 @@ def _ns_iterate(X: torch.Tensor, steps: int) -> torch.Tensor:
         X = torch.baddbmm(X, Bm, X, beta=a, alpha=1.0)
     for _ in range(2):
         X = torch.baddbmm(X, gram(X), X, beta=1.5, alpha=-0.5)
-    return X
+    return [X]
 
 
 def newton_schulz_5(G: torch.Tensor, steps: int = 5, eps: float = 1e-7,
@@ -235,6 +283,7 @@ def _newton_schulz_unscaled(Gs, steps, eps, ns_dtype):
             X = _mT(X.to(F32))
         groups.setdefault(tuple(X.shape[-2:]), []).append((i, X))
     out = [None] * len(Gs)
+    batches = []
     for items in groups.values():
         # each matrix normalised straight into its slice of the batch
         k_all = sum(x.shape[0] for _, x in items)
@@ -244,7 +293,12 @@ def _newton_schulz_unscaled(Gs, steps, eps, ns_dtype):
         for _, x in items:
             _normalize_into(x, batch[k0:k0 + x.shape[0]], eps)
             k0 += x.shape[0]
-        Y = _ns_iterate(batch, steps)
+        batches.append(batch)
+    # the shape groups iterate together, four per GEMM launch
+    Ys = []
+    for i in range(0, len(batches), 4):
+        Ys += _ns_iterate_many(batches[i:i + 4], steps)
+    for items, Y in zip(groups.values(), Ys):
         k0 = 0
         for i, x in items:
             y = Y[k0:k0 + x.shape[0]]

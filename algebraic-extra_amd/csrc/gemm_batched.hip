@@ -6,6 +6,8 @@
 // formed), b A + c A A and a X + B X (the second operand [k][n], read through
 // transposing LDS reads), each written to its own buffer with the
 // combination in the epilogue.
+#include <utility>
+
 #include "gemm_core.h"
 
 namespace algx {
@@ -23,6 +25,16 @@ struct BatchGemm {
   int tiles_m, tiles_n;
   int batch;
   int ntiles;  // tiles per matrix (upper triangle only when symmetric)
+};
+
+// Up to kMaxGroups batches of one launch. Group i owns workgroups
+// [start[i], start[i + 1]); every start is a multiple of 8, so a workgroup's
+// XCD (index mod 8) is the same counted from the launch or from its group.
+constexpr int kMaxGroups = 4;
+struct GemmGroups {
+  BatchGemm g[kMaxGroups];
+  int start[kMaxGroups + 1];
+  int ngroups;
 };
 
 // Workgroup b -> (matrix, tile). Workgroups are dealt to the 8 XCDs
@@ -97,12 +109,18 @@ __device__ __forceinline__ void store_tile(const BatchGemm& p, int mat, int m0, 
 // above the diagonal are formed; an off-diagonal tile's values also go to
 // the mirrored tile, transposed through the idle stage buffers.
 template <bool AKC, bool BKC, bool DMA, bool SYM>
-__global__ __launch_bounds__(kThreads) void batched_gemm_kernel(BatchGemm p) {
+__global__ __launch_bounds__(kThreads) void batched_gemm_kernel(GemmGroups gp) {
   GEMM_LDS_STAGES;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
-  const int wm = w / NWN, wn = w % NWN;
+  const int tid = threadIdx.x;
+  int gi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxGroups; ++i)
+    if (i < gp.ngroups && (int)blockIdx.x >= gp.start[i]) gi = i;
+  const BatchGemm p = gp.g[gi];
+  const int local = (int)blockIdx.x - gp.start[gi];
+  if (local >= p.batch * p.ntiles) return;  // padding of the group to a multiple of 8
   int mat, tile;
-  batch_tile(blockIdx.x, p, mat, tile);
+  batch_tile(local, p, mat, tile);
   int n0, m0;
   if (SYM) {
     int a, b;
@@ -149,7 +167,7 @@ __global__ __launch_bounds__(kThreads) void batched_gemm_kernel(BatchGemm p) {
   }
 }
 
-typedef void (*BatchFn)(BatchGemm);
+typedef void (*BatchFn)(GemmGroups);
 template <bool DMA, bool SYM> BatchFn pick_batched_as(bool akc, bool bkc) {
   if (akc)
     return bkc ? batched_gemm_kernel<true, true, DMA, SYM> : batched_gemm_kernel<true, false, DMA, SYM>;
@@ -161,6 +179,102 @@ BatchFn pick_batched(bool akc, bool bkc, bool dma, bool sym) {
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Checks one batch's arguments and fills its descriptor (tile counts are set
+// by the launch, which knows whether the symmetric schedule runs).
+int32_t fill_batch(const algx_gemm_batch& b, bool a_kc, bool b_kc, bool symmetric, float alpha,
+                   float beta, BatchGemm& p) {
+  if (b.batch < 0 || b.M < 0 || b.N < 0 || b.K < 0) return fail("gemm_bf16_batched: negative size");
+  p = BatchGemm{};
+  p.batch = b.batch;
+  p.M = b.M;
+  p.N = b.N;
+  p.K = b.K;
+  if (b.batch == 0 || b.M == 0 || b.N == 0) return 0;  // nothing to form
+  if (b.A == nullptr || b.B == nullptr || b.C == nullptr) return fail("gemm_bf16_batched: null pointer");
+  // Every operand is moved in 16-byte chunks along its contiguous axis.
+  if (b.M % 8 || b.N % 8 || b.K % 8)
+    return fail("gemm_bf16_batched: M, N and K must be multiples of 8");
+  const bool d = b.D != nullptr;
+  if (b.lda % 8 || b.ldb % 8 || b.ldc % 8 || (d && b.ldd % 8) || b.stride_a % 8 ||
+      b.stride_b % 8 || (d && b.stride_d % 8) || b.stride_c % 8)
+    return fail("gemm_bf16_batched: leading dimensions and batch strides must be multiples of 8");
+  if (!aligned16(b.A) || !aligned16(b.B) || !aligned16(b.C) || (d && !aligned16(b.D)))
+    return fail("gemm_bf16_batched: operands must be 16-byte aligned");
+  if (b.lda < (a_kc ? b.K : b.M) || b.ldb < (b_kc ? b.K : b.N) || b.ldc < b.N || (d && b.ldd < b.N))
+    return fail("gemm_bf16_batched: leading dimension below the row length");
+  if (b.K == 0) return fail("gemm_bf16_batched: K must be positive");
+  if (symmetric && b.M != b.N) return fail("gemm_bf16_batched: a symmetric product needs M == N");
+  p.A = (const bf16*)b.A;
+  p.B = (const bf16*)b.B;
+  p.D = (const bf16*)b.D;
+  p.C = (bf16*)b.C;
+  p.lda = b.lda;
+  p.ldb = b.ldb;
+  p.ldd = b.ldd;
+  p.ldc = b.ldc;
+  p.sa = b.stride_a;
+  p.sb = b.stride_b;
+  p.sd = b.stride_d;
+  p.sc = b.stride_c;
+  p.alpha = alpha;
+  p.beta = beta;
+  p.tiles_m = (b.M + BN - 1) / BN;  // the kernel's N tiles
+  p.tiles_n = (b.N + BM - 1) / BM;  // the kernel's M tiles
+  return 0;
+}
+
+// One launch over live groups of one stage kind.
+int32_t launch_kind(BatchGemm* all, int live, bool a_kc, bool b_kc, bool dma, bool symmetric,
+                    hipStream_t s) {
+  // the triangle-only schedule of a symmetric C stages its mirrored tiles in
+  // the direct-to-LDS stage buffers (without them every tile is formed)
+  const bool sym = symmetric && dma;
+  // Longest k loops first, so the short ones fill the launch's tail.
+  for (int i = 1; i < live; ++i)
+    for (int j = i; j > 0 && all[j].K > all[j - 1].K; --j) std::swap(all[j], all[j - 1]);
+  GemmGroups gp{};
+  int64_t start = 0;
+  for (int i = 0; i < live; ++i) {
+    BatchGemm& p = all[i];
+    p.ntiles = sym ? p.tiles_m * (p.tiles_m + 1) / 2 : p.tiles_m * p.tiles_n;
+    gp.g[i] = p;
+    gp.start[i] = (int)start;
+    start += ((int64_t)p.batch * p.ntiles + 7) / 8 * 8;
+    if (start > 0x7fffffff) return fail("gemm_bf16_batched: too many tiles");
+  }
+  gp.start[live] = (int)start;
+  gp.ngroups = live;
+  hipLaunchKernelGGL(pick_batched(a_kc, b_kc, dma, sym), dim3((unsigned)start), dim3(kThreads),
+                     0, s, gp);
+  return check_launch("gemm_bf16_batched");
+}
+
+// Groups whose K is a whole number of 32-wide stages run direct-to-LDS, the
+// others register-staged, as in one call per group; the two kinds go to
+// separate launches so that every group takes the path its own call takes.
+int32_t launch_groups(const algx_gemm_batch* groups, int ngroups, bool a_kc, bool b_kc,
+                      bool symmetric, float alpha, float beta, hipStream_t s) {
+  if (ngroups < 0 || ngroups > kMaxGroups)
+    return fail("gemm_bf16_grouped: between 0 and 4 groups");
+  if (ngroups > 0 && groups == nullptr) return fail("gemm_bf16_grouped: null group array");
+  BatchGemm dma[kMaxGroups], reg[kMaxGroups];
+  int nd = 0, nr = 0;
+  for (int i = 0; i < ngroups; ++i) {
+    BatchGemm p;
+    if (int32_t rc = fill_batch(groups[i], a_kc, b_kc, symmetric, alpha, beta, p)) return rc;
+    if (p.batch == 0 || p.M == 0 || p.N == 0) continue;
+    if (p.K % BK == 0)
+      dma[nd++] = p;
+    else
+      reg[nr++] = p;
+  }
+  if (nd > 0)
+    if (int32_t rc = launch_kind(dma, nd, a_kc, b_kc, true, symmetric, s)) return rc;
+  if (nr > 0)
+    if (int32_t rc = launch_kind(reg, nr, a_kc, b_kc, false, symmetric, s)) return rc;
+  return 0;
+}
 
 }  // namespace
 }  // namespace algx
@@ -174,51 +288,15 @@ extern "C" int32_t algx_gemm_bf16_batched(const void* A, const void* B, const vo
                                           int64_t ldd, int64_t ldc, int64_t stride_a,
                                           int64_t stride_b, int64_t stride_d, int64_t stride_c,
                                           float alpha, float beta, void* stream) {
-  if (batch < 0 || M < 0 || N < 0 || K < 0) return fail("gemm_bf16_batched: negative size");
-  if (batch == 0 || M == 0 || N == 0) return 0;
-  if (A == nullptr || B == nullptr || C == nullptr) return fail("gemm_bf16_batched: null pointer");
-  // Every operand is moved in 16-byte chunks along its contiguous axis.
-  if (M % 8 || N % 8 || K % 8) return fail("gemm_bf16_batched: M, N and K must be multiples of 8");
-  if (lda % 8 || ldb % 8 || ldc % 8 || (D != nullptr && ldd % 8) || stride_a % 8 ||
-      stride_b % 8 || (D != nullptr && stride_d % 8) || stride_c % 8)
-    return fail("gemm_bf16_batched: leading dimensions and batch strides must be multiples of 8");
-  if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (D != nullptr && !aligned16(D)))
-    return fail("gemm_bf16_batched: operands must be 16-byte aligned");
-  if (lda < (a_kc ? K : M) || ldb < (b_kc ? K : N) || ldc < N || (D != nullptr && ldd < N))
-    return fail("gemm_bf16_batched: leading dimension below the row length");
-  if (K == 0) return fail("gemm_bf16_batched: K must be positive");
-  BatchGemm p;
-  p.A = (const bf16*)A;
-  p.B = (const bf16*)B;
-  p.D = (const bf16*)D;
-  p.C = (bf16*)C;
-  p.lda = lda;
-  p.ldb = ldb;
-  p.ldd = ldd;
-  p.ldc = ldc;
-  p.sa = stride_a;
-  p.sb = stride_b;
-  p.sd = stride_d;
-  p.sc = stride_c;
-  p.M = M;
-  p.N = N;
-  p.K = K;
-  p.alpha = alpha;
-  p.beta = beta;
-  p.tiles_m = (M + BN - 1) / BN;  // the kernel's N tiles
-  p.tiles_n = (N + BM - 1) / BM;  // the kernel's M tiles
-  p.batch = batch;
-  if (symmetric && M != N) return fail("gemm_bf16_batched: a symmetric product needs M == N");
-  // Direct-to-LDS stages when K is a whole number of 32-wide stages; the
-  // triangle-only schedule of a symmetric C stages its mirrored tiles in
-  // their buffers (without them every tile is formed).
-  const bool dma = K % BK == 0;
-  const bool sym = symmetric && dma;
-  p.ntiles = sym ? p.tiles_m * (p.tiles_m + 1) / 2 : p.tiles_m * p.tiles_n;
-  const int64_t ntot = (int64_t)batch * p.ntiles;
-  if (ntot > 0x7fffffff) return fail("gemm_bf16_batched: too many tiles");
-  hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(pick_batched(a_kc != 0, b_kc != 0, dma, sym), dim3((unsigned)ntot),
-                     dim3(kThreads), 0, s, p);
-  return check_launch("gemm_bf16_batched");
+  const algx_gemm_batch g{A, B, D, C, batch, M, N, K, lda, ldb, ldd, ldc,
+                          stride_a, stride_b, stride_d, stride_c};
+  return launch_groups(&g, 1, a_kc != 0, b_kc != 0, symmetric != 0, alpha, beta,
+                       (hipStream_t)stream);
+}
+
+extern "C" int32_t algx_gemm_bf16_grouped(const algx_gemm_batch* groups, int32_t ngroups,
+                                          int32_t a_kc, int32_t b_kc, int32_t symmetric,
+                                          float alpha, float beta, void* stream) {
+  return launch_groups(groups, ngroups, a_kc != 0, b_kc != 0, symmetric != 0, alpha, beta,
+                       (hipStream_t)stream);
 }

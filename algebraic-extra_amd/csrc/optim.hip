@@ -132,7 +132,21 @@ __global__ __launch_bounds__(kThreads) void ns_sumsq_kernel(const float* __restr
   const int64_t hi = min(mn, lo + span);
   float s0 = 0.0f, s1 = 0.0f;
   if (VEC) {
-    for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 4 * kThreads) {
+    int64_t i = lo + 4 * threadIdx.x;
+    // four 16-byte loads in flight per thread (hi - i is a multiple of 4)
+    for (; i + 12 * kThreads < hi; i += 16 * kThreads) {
+      f32x4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4*>(xk + i + 4 * kThreads * u);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        s0 = __builtin_fmaf(v[u][0], v[u][0], s0);
+        s1 = __builtin_fmaf(v[u][1], v[u][1], s1);
+        s0 = __builtin_fmaf(v[u][2], v[u][2], s0);
+        s1 = __builtin_fmaf(v[u][3], v[u][3], s1);
+      }
+    }
+    for (; i < hi; i += 4 * kThreads) {
       const f32x4 v = *reinterpret_cast<const f32x4*>(xk + i);
       s0 = __builtin_fmaf(v[0], v[0], s0);
       s1 = __builtin_fmaf(v[1], v[1], s1);
@@ -176,8 +190,7 @@ __global__ __launch_bounds__(kThreads) void ns_scale_kernel(const float* __restr
   const int64_t lo = blockIdx.x * span;
   const int64_t hi = min(mn, lo + span);
   if (VEC) {
-    for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 4 * kThreads) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(xk + i);
+    auto put = [&](int64_t i, const f32x4& v) {
       if (sizeof(T) == 2) {
         bf16x4 o;
 #pragma unroll
@@ -189,7 +202,17 @@ __global__ __launch_bounds__(kThreads) void ns_scale_kernel(const float* __restr
         for (int e = 0; e < 4; ++e) o[e] = v[e] / norm;
         *reinterpret_cast<f32x4*>(ok + i) = o;
       }
+    };
+    int64_t i = lo + 4 * threadIdx.x;
+    // four 16-byte loads in flight per thread (hi - i is a multiple of 4)
+    for (; i + 12 * kThreads < hi; i += 16 * kThreads) {
+      f32x4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4*>(xk + i + 4 * kThreads * u);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) put(i + 4 * kThreads * u, v[u]);
     }
+    for (; i < hi; i += 4 * kThreads) put(i, *reinterpret_cast<const f32x4*>(xk + i));
   } else {
     for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) ok[i] = from_f<T>(xk[i] / norm);
   }

@@ -432,6 +432,47 @@ def run_once(which, dev, steps=3):
     torch.cuda.synchronize()
 
 
+def bench_newton_schulz(steps, warmup, dev):
+    """Muon's Newton-Schulz at the 350M model's shapes: the 96 [1024, 1024]
+    and 72 [1024, 2688] matrices of one training step (optimizers.py:27-65,
+    5 quintic and 2 refinement steps, bf16 products). `iteration_ms` is the
+    products alone (both batches in lockstep, one grouped launch per
+    product); `ms` is newton_schulz_many end to end (float32 in, the
+    normalisation, float32 out). FLOPs count full products (28 m^2 n + 10 m^3
+    per matrix), though the symmetric ones form only their upper triangle."""
+    import torch
+    from algebraic_amd import optimizers as O
+    gen = torch.Generator(device=dev).manual_seed(4)
+    Gs = [torch.randn((96, 1024, 1024), device=dev, generator=gen),
+          torch.randn((72, 1024, 2688), device=dev, generator=gen)]
+    Xs = []
+    for G in Gs:
+        X = torch.empty(G.shape, dtype=torch.bfloat16, device=dev)
+        O._normalize_into(G, X, 1e-7)
+        Xs.append(X)
+    work = [X.clone() for X in Xs]
+
+    def iteration():
+        for w, X in zip(work, Xs):
+            w.copy_(X)
+        O._ns_iterate_many(work, 5)
+
+    def copies():
+        for w, X in zip(work, Xs):
+            w.copy_(X)
+
+    it_s = time_steps(iteration, steps, warmup)
+    copy_s = time_steps(copies, steps, warmup, settle_s=0.0)
+    full_s = time_steps(lambda: O.newton_schulz_many(Gs), steps, warmup, settle_s=0.0)
+    flops = sum(G.shape[0] * (28 * G.shape[1] ** 2 * G.shape[2] + 10 * G.shape[1] ** 3)
+                for G in Gs)
+    it_ms = (it_s - copy_s) * 1e3
+    return {"workload": "Muon Newton-Schulz, 96 x [1024,1024] + 72 x [1024,2688], bf16, 5+2 steps",
+            "iteration_ms": it_ms, "ms": full_s * 1e3,
+            "iteration_tflops": flops / it_ms / 1e9,
+            "iteration_frac": flops / it_ms / 1e9 / PEAK_BF16_TFLOPS}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -445,6 +486,8 @@ def main():
                     help="print only the 350M model lines (algebraic and standard)")
     ap.add_argument("--elementwise-only", action="store_true",
                     help="print only the rms_norm / alu_glu line")
+    ap.add_argument("--ns-only", action="store_true",
+                    help="print only the Newton-Schulz line (Muon at the 350M model's shapes)")
     ap.add_argument("--once", choices=("attn", "attn16", "head", "qknorm"),
                     help="run three untimed steps of one workload and exit, printing nothing "
                          "else: the command for rocprofv3 counter passes (configs[1] attention, "
@@ -488,6 +531,11 @@ def main():
     if args.elementwise_only:
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
                           for k, v in bench_elementwise(args.steps, args.warmup, dev).items()}),
+              flush=True)
+        return
+    if args.ns_only:
+        print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
+                          for k, v in bench_newton_schulz(args.steps, args.warmup, dev).items()}),
               flush=True)
         return
     torch.cuda.synchronize()
@@ -544,6 +592,8 @@ def main():
                        for k, v in bench_qknorm(20, 3, dev).items()},
             "elementwise": {k: (round(v, 4) if isinstance(v, float) else v)
                             for k, v in bench_elementwise(20, 3, dev).items()},
+            "newton_schulz": {k: (round(v, 4) if isinstance(v, float) else v)
+                              for k, v in bench_newton_schulz(5, 2, dev).items()},
         }
         for preset, remat, opt in (("algebraic", False, False), ("standard", False, False),
                                    ("algebraic", True, False), ("algebraic", False, True)):

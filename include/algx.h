@@ -344,6 +344,28 @@ int32_t algx_gemm_bf16_batched(const void* A, const void* B, const void* D, void
                                int64_t ldd, int64_t ldc, int64_t stride_a, int64_t stride_b,
                                int64_t stride_d,
                                int64_t stride_c, float alpha, float beta, void* stream);
+/* algx_gemm_bf16_grouped: up to 4 batches of algx_gemm_bf16_batched products
+ * in one launch (the operands, sizes and strides of each group its own; the
+ * operand layouts, symmetry and alpha/beta shared). Muon orthogonalises
+ * matrices of several shapes at each step (newton_schulz_5,
+ * src/algebraic/optimizers.py:27-65, called per Muon weight at :202): one
+ * launch per product over all of them fills the
+ * tail of each group's last round of workgroups with the others' tiles.
+ * Results equal one algx_gemm_bf16_batched call per group, bit for bit
+ * (groups whose K is not a multiple of 32 run in a second launch, on the
+ * register-staged path their own call takes). */
+typedef struct algx_gemm_batch {
+  const void* A;
+  const void* B;
+  const void* D; /* may be null (no beta term) or equal to C */
+  void* C;
+  int32_t batch, M, N, K;
+  int64_t lda, ldb, ldd, ldc;
+  int64_t stride_a, stride_b, stride_d, stride_c;
+} algx_gemm_batch;
+int32_t algx_gemm_bf16_grouped(const algx_gemm_batch* groups, int32_t ngroups, int32_t a_kc,
+                               int32_t b_kc, int32_t symmetric, float alpha, float beta,
+                               void* stream);
 
 #ifdef __cplusplus
 }

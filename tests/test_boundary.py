@@ -77,6 +77,23 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert rc != 0 and b"16-byte aligned" in lib.algx_last_error()
 
 
+def test_grouped_gemm_validation_without_a_gpu():
+    """algx_gemm_bf16_grouped checks the group count and every group's
+    arguments before it launches; empty groups launch nothing."""
+    lib = _lib.load()
+    arr = (_lib.GemmBatch * 5)()
+    rc = lib.algx_gemm_bf16_grouped(arr, 5, 1, 1, 0, 1.0, 0.0, None)
+    assert rc != 0 and b"between 0 and 4" in lib.algx_last_error()
+    assert lib.algx_gemm_bf16_grouped(arr, 0, 1, 1, 0, 1.0, 0.0, None) == 0
+    assert lib.algx_gemm_bf16_grouped(arr, 2, 1, 1, 0, 1.0, 0.0, None) == 0  # batch 0
+    arr[1] = _lib.GemmBatch(16, 16, None, 16, 2, 12, 16, 32, 32, 32, 16, 16, 384, 512, 0, 192)
+    rc = lib.algx_gemm_bf16_grouped(arr, 2, 1, 1, 0, 1.0, 0.0, None)
+    assert rc != 0 and b"multiples of 8" in lib.algx_last_error()
+    arr[1] = _lib.GemmBatch(16, 16, None, 16, 2, 16, 24, 32, 32, 32, 24, 24, 512, 768, 0, 384)
+    rc = lib.algx_gemm_bf16_grouped(arr, 2, 1, 1, 1, 1.0, 0.0, None)
+    assert rc != 0 and b"M == N" in lib.algx_last_error()
+
+
 def _t(shape, dtype=torch.bfloat16):
     return torch.zeros(shape, dtype=dtype)
 

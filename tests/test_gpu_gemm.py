@@ -106,3 +106,69 @@ def test_batched_gemm_symmetric_needs_square():
     with pytest.raises(RuntimeError, match="M == N"):
         O.gemm_bf16_batched(A, B, a_kc=True, b_kc=True, symmetric=True)
 
+
+
+@pytest.mark.parametrize("a_kc,b_kc,sym", [(True, True, True), (True, False, True),
+                                          (True, False, False), (False, True, False),
+                                          (False, False, False)])
+def test_grouped_launch_equals_one_call_per_batch(a_kc, b_kc, sym):
+    """algx_gemm_bf16_grouped: batches of different shapes (ragged tiles,
+    batch counts that do and do not take the XCD-grouped order, K of both
+    stage kinds when not symmetric) in one launch give exactly what one
+    algx_gemm_bf16_batched call per batch gives."""
+    g = torch.Generator(device=DEV).manual_seed(11 + 2 * a_kc + b_kc + 4 * sym)
+    shapes = ([(8, 264, 264, 96), (3, 520, 520, 200), (16, 256, 256, 64)] if sym else
+              [(8, 264, 520, 96), (3, 40, 8, 72), (5, 520, 264, 200), (16, 256, 256, 1024)])
+    problems = []
+    for batch, M, N, K in shapes:
+        A = torch.randn((batch, M, K) if a_kc else (batch, K, M), generator=g, device=DEV).bfloat16()
+        if sym:
+            B = A
+        else:
+            B = torch.randn((batch, N, K) if b_kc else (batch, K, N), generator=g, device=DEV).bfloat16()
+        D = torch.randn((batch, M, N), generator=g, device=DEV)
+        if sym:
+            D = (D + D.transpose(1, 2)) * 0.5
+        problems.append((A, B, D.bfloat16().contiguous()))
+    if sym and not b_kc:
+        # c A A + b A with A symmetric (the Newton-Schulz form)
+        problems = [(D, D, D) for _, _, D in problems]
+    outs = O.gemm_bf16_grouped([(A, B, D, None) for A, B, D in problems], a_kc=a_kc, b_kc=b_kc,
+                               alpha=-0.75, beta=1.25, symmetric=sym)
+    for (A, B, D), got in zip(problems, outs):
+        want = O.gemm_bf16_batched(A, B, a_kc=a_kc, b_kc=b_kc, D=D, alpha=-0.75, beta=1.25,
+                                   symmetric=sym)
+        assert torch.equal(got, want)
+    # without D, and a single group
+    outs = O.gemm_bf16_grouped([(A, B, None, None) for A, B, _ in problems[:1]], a_kc=a_kc,
+                               b_kc=b_kc, symmetric=sym)
+    A, B, _ = problems[0]
+    assert torch.equal(outs[0], O.gemm_bf16_batched(A, B, a_kc=a_kc, b_kc=b_kc, symmetric=sym))
+
+
+def test_grouped_launch_rejects():
+    A = torch.zeros((2, 16, 32), device=DEV, dtype=torch.bfloat16)
+    B = torch.zeros((2, 24, 32), device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="M == N"):
+        O.gemm_bf16_grouped([(A, A, None, None), (A, B, None, None)], a_kc=True, b_kc=True,
+                            symmetric=True)
+    with pytest.raises(ValueError, match="at most 4"):
+        O.gemm_bf16_grouped([(A, A, None, None)] * 5, a_kc=True, b_kc=True)
+    with pytest.raises(ValueError, match="beta needs"):
+        O.gemm_bf16_grouped([(A, A, None, None)], a_kc=True, b_kc=True, beta=1.0)
+    assert O.gemm_bf16_grouped([], a_kc=True, b_kc=True) == []
+
+
+def test_newton_schulz_groups_in_lockstep_equal_separate_runs():
+    """newton_schulz_many iterates its shape groups together (one grouped
+    launch per product): the result equals each batch iterated alone."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    Xs = []
+    for shape in ((16, 1024, 1024), (8, 1024, 2688), (3, 264, 520)):
+        G = torch.randn(shape, generator=g, device=DEV)
+        X = torch.empty(shape, dtype=torch.bfloat16, device=DEV)
+        O._normalize_into(G, X, 1e-7)
+        Xs.append(X)
+    together = O._ns_iterate_many([X.clone() for X in Xs], 5)
+    for X, got in zip(Xs, together):
+        assert torch.equal(got, O._ns_iterate(X.clone(), 5))
