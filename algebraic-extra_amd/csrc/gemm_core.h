@@ -34,6 +34,12 @@ struct Operand {
   int64_t ld;
   int rows;  // extent along m (or n)
   int K;
+  // 0: plain row-major storage. Otherwise the operand is stored in blocks of
+  // 32 contiguous columns of the row-major matrix ([cols / 32][rows][32],
+  // ld = 32) and bstride is the distance between blocks; the direct-to-LDS
+  // path reads it (whole 64-byte row pieces per 32-wide k stage), the
+  // register-staged path does not.
+  int64_t bstride = 0;
 };
 
 // Stages one 256 x 64 (mn x k) tile of an operand into registers (zero
@@ -231,8 +237,16 @@ __device__ __forceinline__ const bf16* dma_src(const Operand& op, int mn0, int b
   } else {
     const int r = 2 * blk + (lane >> 5), c = (lane & 31) ^ (4 * (r & 3));
     const int col = mn0 + 8 * c;
-    return col < op.rows ? op.p + (int64_t)r * op.ld + col : op.p;
+    const int64_t at = op.bstride ? (int64_t)(col >> 5) * op.bstride + (col & 31) : col;
+    return col < op.rows ? op.p + (int64_t)r * op.ld + at : op.p;
   }
+}
+
+// Elements between consecutive 32-wide k stages of an operand.
+template <bool KC>
+__device__ __forceinline__ int64_t kstep(const Operand& op) {
+  if (KC) return op.bstride ? op.bstride : BK;  // the next 32-column block
+  return (int64_t)BK * op.ld;                    // the next 32 rows
 }
 
 // MFMA operand (as `operand`) from a swizzled DMA stage.
@@ -406,7 +420,7 @@ __device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B,
   const bf16* b0 = dma_src<BKC>(B, n0, 2 * w, lane);
   const bf16* b1 = dma_src<BKC>(B, n0, 2 * w + 1, lane);
   gemm_stream_dma<AKC, BKC>(
-      A.K / BK, AKC ? BK : (int64_t)BK * A.ld, BKC ? BK : (int64_t)BK * B.ld, ntiles,
+      A.K / BK, kstep<AKC>(A), kstep<BKC>(B), ntiles,
       [&](int t, const bf16*& a0, const bf16*& a1, const bf16*& sb0, const bf16*& sb1) {
         a0 = dma_src<AKC>(A, m0 + t * BM, 2 * w, lane);
         a1 = dma_src<AKC>(A, m0 + t * BM, 2 * w + 1, lane);

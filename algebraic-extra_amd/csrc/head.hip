@@ -208,12 +208,15 @@ __global__ __launch_bounds__(256) void head_stat_kernel(const float* __restrict_
 }
 
 // dz tile of a token chunk: dz[t][v] = bf16(f(z) * scale), 0 for padded v.
+// bstride = 0: dz row-major with row stride ldz. Otherwise dz is stored in
+// blocks of 32 vocabulary columns, [v / 32][t][32] with blocks bstride apart
+// (the layout the backward's GEMMs read in whole 64-byte row pieces).
 template <int KIND, int L2N, bool DMA>
 __global__ __launch_bounds__(kThreads) void head_dz_kernel(
     const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
     const float* __restrict__ stat, const float* __restrict__ scale, bf16* __restrict__ dz,
-    int64_t ldz, int tok0, int ntok, int d, int V, int log2n, float inv_c, float clamp,
-    int chunk_tiles) {
+    int64_t ldz, int64_t bstride, int tok0, int ntok, int d, int V, int log2n, float inv_c,
+    float clamp, int chunk_tiles) {
   GEMM_LDS_STAGES;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
   const int wm = w / NWN, wn = w % NWN;
@@ -266,7 +269,9 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
             }
             out[u] = (bf16)((FULL || m < V) ? g_z * sc : 0.0f);
           }
-          *reinterpret_cast<bf16x4*>(dz + (int64_t)tl * ldz + mb) = out;
+          const int64_t at = bstride ? (int64_t)(mb >> 5) * bstride + (int64_t)tl * 32 + (mb & 31)
+                                     : (int64_t)tl * ldz + mb;
+          *reinterpret_cast<bf16x4*>(dz + at) = out;
         }
     }
   };
@@ -378,7 +383,7 @@ int32_t check_head(const void* h, const void* E, const int32_t* targets, int N, 
 typedef void (*HeadFwdFn)(const bf16*, const bf16*, const int32_t*, float*, float*, int, int,
                           int, int, float, float, int);
 typedef void (*HeadDzFn)(const bf16*, const bf16*, const int32_t*, const float*, const float*,
-                         bf16*, int64_t, int, int, int, int, int, float, float, int);
+                         bf16*, int64_t, int64_t, int, int, int, int, int, float, float, int);
 
 // Kernel instance for (kind, n): alg_ce with n = 8, 16 or 32 gets unrolled
 // powers. DMA (the direct-to-LDS ring) when d is a multiple of BK.
@@ -498,25 +503,30 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
   for (int tok0 = 0; tok0 < N; tok0 += csize) {
     const int ntok = min(csize, N - tok0);
     const int ct = chunk_tiles_of(ntok, V);
+    // LDS-DMA stages in the dh/dE launch when both products have whole k
+    // stages (V and the chunk's token count multiples of BK). dz is then
+    // stored in 32-column blocks ([v / 32][t][32]): dh's 32-wide k stage
+    // reads one 64-byte piece per token row, dE's reads 32 token rows of one
+    // block contiguously (2 KB), instead of half lines of 100 KB rows.
+    const bool dma = V % BK == 0 && ntok % BK == 0;
+    const int64_t bstride = dma ? (int64_t)32 * ntok : 0;
     dim3 gdz((ntok + BN - 1) / BN, ((V + BM - 1) / BM + ct - 1) / ct);
     launch_k(probe_for(ALGX_PROBE_HEAD_DZ),
              pick_head_dz(kind, log2n, d),
-             gdz, dim3(kThreads), s, hb, eb, targets, stat, scale, dz, ldz, tok0, ntok, d, V, log2n,
-             inv_c, clamp, ct);
+             gdz, dim3(kThreads), s, hb, eb, targets, stat, scale, dz, ldz, bstride, tok0, ntok, d,
+             V, log2n, inv_c, clamp, ct);
     if (int32_t rc = check_launch("head_dz")) return rc;
     // dh[t][c] = sum_v dz[t][v] E[v][c]: A = dz (k-contiguous), B(n=c,k=v) = E stored [v][c].
     // dE[v][c] (+)= sum_t dz[t][v] h[t][c]: A(m=v,k=t) = dz stored [t][v], B(n=c,k=t) = h [t][c].
     const int tn = (d + BN - 1) / BN;
-    const GemmJob jdh{Operand{dz, ldz, ntok, V}, Operand{eb, d, d, V},
-                      (bf16*)dh + (int64_t)tok0 * d, (int64_t)d, ntok, d, tn};
-    const GemmJob jde{Operand{dz, ldz, V, ntok}, Operand{hb + (int64_t)tok0 * d, d, d, ntok},
-                      dE, (int64_t)d, V, d, tn};
+    const Operand dz_t = dma ? Operand{dz, 32, ntok, V, bstride} : Operand{dz, ldz, ntok, V};
+    const Operand dz_v = dma ? Operand{dz, 32, V, ntok, bstride} : Operand{dz, ldz, V, ntok};
+    const GemmJob jdh{dz_t, Operand{eb, d, d, V}, (bf16*)dh + (int64_t)tok0 * d, (int64_t)d,
+                      ntok, d, tn};
+    const GemmJob jde{dz_v, Operand{hb + (int64_t)tok0 * d, d, d, ntok}, dE, (int64_t)d, V, d, tn};
     const int n_dh = ((ntok + BM - 1) / BM) * tn;
     const int n_de = ((V + BM - 1) / BM) * tn;
     const int dh_slots = (n_dh + 7) / 8 * 8;
-    // LDS-DMA stages when both products have whole k stages (V and the
-    // chunk's token count multiples of BK).
-    const bool dma = V % BK == 0 && ntok % BK == 0;
     auto gk = dma ? (tok0 == 0 ? head_grad_kernel<false, true> : head_grad_kernel<true, true>)
                   : (tok0 == 0 ? head_grad_kernel<false, false> : head_grad_kernel<true, false>);
     launch_k(probe_for(ALGX_PROBE_HEAD_DE), gk, dim3(dh_slots + n_de), dim3(kThreads), s, jdh, jde,
