@@ -208,10 +208,10 @@ __global__ __launch_bounds__(256) void head_stat_kernel(const float* __restrict_
 }
 
 // dz tile of a token chunk: dz[t][v] = bf16(f(z) * scale), 0 for padded v.
-// bstride = 0: dz row-major with row stride ldz. Otherwise dz is stored in
-// blocks of 32 vocabulary columns, [v / 32][t][32] with blocks bstride apart
-// (the layout the backward's GEMMs read in whole 64-byte row pieces).
-template <int KIND, int L2N, bool DMA>
+// BLK = false: dz row-major with row stride ldz. BLK: dz is stored in blocks
+// of 32 vocabulary columns, [v / 32][t][32] with blocks bstride apart (the
+// layout the backward's GEMMs read in whole 64-byte row pieces).
+template <int KIND, int L2N, bool DMA, bool BLK>
 __global__ __launch_bounds__(kThreads) void head_dz_kernel(
     const bf16* __restrict__ h, const bf16* __restrict__ e, const int32_t* __restrict__ targets,
     const float* __restrict__ stat, const float* __restrict__ scale, bf16* __restrict__ dz,
@@ -241,38 +241,62 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
   // vocabulary tile), so no row mask is formed.
   auto emit = [&](auto full_tag, int m0, const Acc& acc) {
     constexpr bool FULL = decltype(full_tag)::value;
+    // dz of columns mb0 + 8 q4 + 4 g .. + 3 of token column j
+    auto run = [&](int mb0, int i, int j, int q4, int tgt, float st) {
+      bf16x4 out;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int m = mb0 + 8 * q4 + 4 * g + u;
+        const float z = acc.v[i][j][4 * q4 + u];
+        const float y = m == tgt ? 1.0f : 0.0f;
+        float g_z;
+        if (KIND == ALGX_HEAD_CE) {
+          g_z = __builtin_amdgcn_exp2f((z - st) * 1.4426950408889634f) - y;
+        } else {
+          const float x = __builtin_fminf(z * inv_c, clamp);
+          float r;
+          const float p = pow_n<L2N>(rho_fast(x, r) * st, log2n);
+          g_z = (p - y) * r;
+        }
+        out[u] = (bf16)((FULL || m < V) ? g_z * sc : 0.0f);
+      }
+      return out;
+    };
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
-      const int tl = n0 + WTN * wn + 32 * j + c32;
-      if (tl >= ntok) continue;
+      const int tl = n0 + WTN * wn + 32 * j + c32;  // the same in lanes c32 and c32 + 32
       const int tgt = tgt_j[j];
       const float st = st_j[j];
 #pragma unroll
-      for (int i = 0; i < TI; ++i)
+      for (int i = 0; i < TI; ++i) {
+        const int mb0 = m0 + WTM * wm + 32 * i;  // a 32-column block of dz
+        if (tl >= ntok) continue;  // both lanes of a swap pair
+        if constexpr (BLK) {
+          // Lanes c32 and c32 + 32 hold alternate 4-column runs of one
+          // token's 32 columns. Per pair of runs, two swaps between the lane
+          // halves give each lane 8 consecutive columns, stored as 16 bytes:
+          // columns 16 h + 8 g .. + 7 of the block.
+          bf16* row = dz + (int64_t)(mb0 >> 5) * bstride + (int64_t)tl * 32 + 8 * g;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const int mb = m0 + WTM * wm + 32 * i + 8 * q4 + 4 * g;
-          bf16x4 out;
+          for (int h = 0; h < 2; ++h) {
+            u32x2 d0 = __builtin_bit_cast(u32x2, run(mb0, i, j, 2 * h, tgt, st));
+            u32x2 d1 = __builtin_bit_cast(u32x2, run(mb0, i, j, 2 * h + 1, tgt, st));
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int m = mb + u;
-            const float z = acc.v[i][j][4 * q4 + u];
-            const float y = m == tgt ? 1.0f : 0.0f;
-            float g_z;
-            if (KIND == ALGX_HEAD_CE) {
-              g_z = __builtin_amdgcn_exp2f((z - st) * 1.4426950408889634f) - y;
-            } else {
-              const float x = __builtin_fminf(z * inv_c, clamp);
-              float r;
-              const float p = pow_n<L2N>(rho_fast(x, r) * st, log2n);
-              g_z = (p - y) * r;
+            for (int e = 0; e < 2; ++e) {
+              // upper half of d0[e] <-> lower half of d1[e]
+              const auto r = __builtin_amdgcn_permlane32_swap(d0[e], d1[e], false, false);
+              d0[e] = r[0];
+              d1[e] = r[1];
             }
-            out[u] = (bf16)((FULL || m < V) ? g_z * sc : 0.0f);
+            *reinterpret_cast<u32x4*>(row + 16 * h) = u32x4{d0[0], d0[1], d1[0], d1[1]};
           }
-          const int64_t at = bstride ? (int64_t)(mb >> 5) * bstride + (int64_t)tl * 32 + (mb & 31)
-                                     : (int64_t)tl * ldz + mb;
-          *reinterpret_cast<bf16x4*>(dz + at) = out;
+        } else {
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            *reinterpret_cast<bf16x4*>(dz + (int64_t)tl * ldz + mb0 + 8 * q4 + 4 * g) =
+                run(mb0, i, j, q4, tgt, st);
         }
+      }
     }
   };
   auto emit_tile = [&](int, int m0, const Acc& a) {
@@ -396,22 +420,24 @@ template <bool DMA> HeadFwdFn pick_head_fwd_as(int kind, int log2n) {
     default: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 0, DMA>;
   }
 }
-template <bool DMA> HeadDzFn pick_head_dz_as(int kind, int log2n) {
-  if (kind == ALGX_HEAD_CE) return head_dz_kernel<ALGX_HEAD_CE, 0, DMA>;
+template <bool DMA, bool BLK> HeadDzFn pick_head_dz_as(int kind, int log2n) {
+  if (kind == ALGX_HEAD_CE) return head_dz_kernel<ALGX_HEAD_CE, 0, DMA, BLK>;
   switch (log2n) {
-    case 3: return head_dz_kernel<ALGX_HEAD_ALG_CE, 3, DMA>;
-    case 4: return head_dz_kernel<ALGX_HEAD_ALG_CE, 4, DMA>;
-    case 5: return head_dz_kernel<ALGX_HEAD_ALG_CE, 5, DMA>;
-    default: return head_dz_kernel<ALGX_HEAD_ALG_CE, 0, DMA>;
+    case 3: return head_dz_kernel<ALGX_HEAD_ALG_CE, 3, DMA, BLK>;
+    case 4: return head_dz_kernel<ALGX_HEAD_ALG_CE, 4, DMA, BLK>;
+    case 5: return head_dz_kernel<ALGX_HEAD_ALG_CE, 5, DMA, BLK>;
+    default: return head_dz_kernel<ALGX_HEAD_ALG_CE, 0, DMA, BLK>;
   }
 }
 HeadFwdFn pick_head_fwd(int kind, int log2n, int d) {
   return d % (BK * kDmaStages) == 0 ? pick_head_fwd_as<true>(kind, log2n)
                                     : pick_head_fwd_as<false>(kind, log2n);
 }
-HeadDzFn pick_head_dz(int kind, int log2n, int d) {
-  return d % (BK * kDmaStages) == 0 ? pick_head_dz_as<true>(kind, log2n)
-                                    : pick_head_dz_as<false>(kind, log2n);
+HeadDzFn pick_head_dz(int kind, int log2n, int d, bool blocked) {
+  const bool dma = d % (BK * kDmaStages) == 0;
+  if (blocked)
+    return dma ? pick_head_dz_as<true, true>(kind, log2n) : pick_head_dz_as<false, true>(kind, log2n);
+  return dma ? pick_head_dz_as<true, false>(kind, log2n) : pick_head_dz_as<false, false>(kind, log2n);
 }
 
 // Vocabulary tiles per forward workgroup: the token blocks x vocabulary tiles
@@ -512,7 +538,7 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
     const int64_t bstride = dma ? (int64_t)32 * ntok : 0;
     dim3 gdz((ntok + BN - 1) / BN, ((V + BM - 1) / BM + ct - 1) / ct);
     launch_k(probe_for(ALGX_PROBE_HEAD_DZ),
-             pick_head_dz(kind, log2n, d),
+             pick_head_dz(kind, log2n, d, bstride != 0),
              gdz, dim3(kThreads), s, hb, eb, targets, stat, scale, dz, ldz, bstride, tok0, ntok, d,
              V, log2n, inv_c, clamp, ct);
     if (int32_t rc = check_launch("head_dz")) return rc;
