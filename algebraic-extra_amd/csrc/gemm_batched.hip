@@ -69,7 +69,10 @@ __device__ __forceinline__ void upper_tile(int idx, int t, int& a, int& b) {
 // C[m][n] (+ beta D) of a finished 256 x 256 tile of C^T at (n0, m0):
 // acc.v[i][j][4q + u] = C[m][n + u], m = m0 + WTN wn + 32 j + c32,
 // n = n0 + WTM wm + 32 i + 8 q + 4 g (N % 8 == 0: a run is whole or absent).
-// Each run's bf16 values also go to mirror(r, col, value4) when given.
+// Each run's bf16 values also go to mirror(r, col, value4) when given. The
+// D runs of one j are all loaded before any is used (outside rows and
+// columns read D's first run instead), so a lane waits for D once per j
+// rather than once per run.
 template <typename Mirror>
 __device__ __forceinline__ void store_tile(const BatchGemm& p, int mat, int m0, int n0,
                                            const Acc& acc, int tid, Mirror&& mirror) {
@@ -80,7 +83,19 @@ __device__ __forceinline__ void store_tile(const BatchGemm& p, int mat, int m0, 
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int m = m0 + WTN * wn + 32 * j + c32;
-    if (m >= p.M) continue;
+    const bool m_in = m < p.M;
+    bf16x4 d[TI][4];
+    if (D != nullptr) {
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + WTM * wm + 32 * i + 8 * q + 4 * g;
+          const int64_t at = m_in && n < p.N ? (int64_t)m * p.ldd + n : 0;
+          d[i][q] = *reinterpret_cast<const bf16x4*>(D + at);
+        }
+    }
+    if (!m_in) continue;
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -91,9 +106,8 @@ __device__ __forceinline__ void store_tile(const BatchGemm& p, int mat, int m0, 
 #pragma unroll
         for (int u = 0; u < 4; ++u) v[u] = p.alpha * acc.v[i][j][4 * q + u];
         if (D != nullptr) {
-          const bf16x4 d = *reinterpret_cast<const bf16x4*>(D + (int64_t)m * p.ldd + n);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) v[u] = __builtin_fmaf(p.beta, (float)d[u], v[u]);
+          for (int u = 0; u < 4; ++u) v[u] = __builtin_fmaf(p.beta, (float)d[i][q][u], v[u]);
         }
         const bf16x4 o = {(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
         *reinterpret_cast<bf16x4*>(C + (int64_t)m * p.ldc + n) = o;
