@@ -29,7 +29,7 @@ __device__ __forceinline__ void fwd_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
     float* __restrict__ stat, int H, int T_, const KVariant& var, const FwdPrep& prep,
-    bf16 (*Ks)[FBN * KSTR], bf16 (*Vs)[FBN * VSTR], float (*red)[4], int bid, int nblocks) {
+    bf16 (*Kr)[FBN * HD], bf16 (*Vr)[FBN * HD], float (*red)[4], int bid, int nblocks) {
   const int nheads = nblocks / (T_ / FBM);
   int bh, qb;
   map_block(bid, nheads, T_ / FBM, true, bh, qb);
@@ -113,59 +113,74 @@ __device__ __forceinline__ void fwd_body(
   zero16(oacc[0]);
   zero16(oacc[1]);
 
-  // Loaders: threads 0..127 move K tiles, 128..255 move V tiles, both kept
-  // row-major ([key][d]) in LDS.
-  bf16x8 pre[4];
-  const bool kloader = tid < 128;
-  const int u = tid & 127;
+  // K and V tiles move straight from global memory into three-slot LDS rings
+  // (tile t in slot t % 3), unpadded rows with chunk c of row r at chunk
+  // c ^ sw16(r). Each wave issues two 1 KB blocks of each tile (rows 16w ..
+  // 16w + 15): lane i of block b fills row 8b + i / 8, physical chunk i % 8,
+  // so it reads logical chunk (i % 8) ^ sw16(row) from global memory.
   const int nkb = (q0 + FBM) / FBN;
-  auto gload = [&](int kb) {
-    const bf16* src = (kloader ? k : v) + base + (int64_t)kb * FBN * HD;
+  unsigned voff[2];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int id = u + 128 * c;
-      pre[c] = *reinterpret_cast<const bf16x8*>(src + (id >> 3) * HD + (id & 7) * 8);
-    }
-  };
-  auto lstore = [&](int buf) {
-    bf16* dst = kloader ? Ks[buf] : Vs[buf];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int id = u + 128 * c;
-      *reinterpret_cast<bf16x8*>(&dst[(id >> 3) * KSTR + (id & 7) * 8]) = pre[c];
-    }
-  };
-  // Tile each loader group fetches in iteration kb (K two ahead, V one ahead).
-  auto my_tile = [&](int kb) { return kloader ? kb + 2 : kb + 1; };
-
-  // Prologue: K_0, K_1 and V_0 in LDS; K_2 / V_1 in flight.
-  if (kloader) {
-    gload(0);
-    lstore(0);
-    if (nkb > 1) {
-      gload(1);
-      lstore(1);
-    }
-  } else {
-    gload(0);
-    lstore(0);
+  for (int h2 = 0; h2 < 2; ++h2) {
+    const int row = 8 * (2 * w + h2) + (lane >> 3);
+    voff[h2] = (unsigned)(row * HD + 8 * ((lane & 7) ^ sw16(row))) * 2u;
   }
-  __syncthreads();
-  if (my_tile(0) < nkb) gload(my_tile(0));
+  const unsigned wblk = 2048u * (unsigned)__builtin_amdgcn_readfirstlane(w);
+  auto issue_k = [&](int t) {
+    const bf16* src = k + base + (int64_t)t * FBN * HD;
+    const unsigned dst = lds_u32(Kr[t % 3]) + wblk;
+    dma16_s(src, voff[0], dst);
+    dma16_s(src, voff[1], dst + 1024);
+  };
+  auto issue_v = [&](int t) {
+    const bf16* src = v + base + (int64_t)t * FBN * HD;
+    const unsigned dst = lds_u32(Vr[t % 3]) + wblk;
+    dma16_s(src, voff[0], dst);
+    dma16_s(src, voff[1], dst + 1024);
+  };
 
+  // Prologue: K_0..K_2 and V_0, V_1 resident; scores of tile 0; then K_3 and
+  // V_2 issued (K_3 replaces K_0). From then on the end of step kb issues
+  // K_{kb+4} and V_{kb+3} into the slots step kb has finished with, and
+  // waits for K_{kb+2} and V_{kb+1} (issued two steps earlier).
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+    if (t < nkb) issue_k(t);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    if (t < nkb) issue_v(t);
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  // A operand of S^T: lane reads K[32 mt + c32][16 ks + 8 g ..] (rows 32 mt
+  // apart share the chunk placement).
+  int koff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) koff[ks] = c32 * HD + 8 * ((2 * ks + g) ^ sw16(c32));
   auto scores = [&](int kb, f32x16 (&s)[2]) {
-    const int buf = kb & 1;
+    const bf16* Kt = Kr[kb % 3];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       zero16(s[mt]);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 a =
-            *reinterpret_cast<const bf16x8*>(&Ks[buf][(32 * mt + c32) * KSTR + 16 * ks + 8 * g]);
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Kt[32 * mt * HD + koff[ks]]);
         s[mt] = mfma32(a, qreg[ks], s[mt]);
       }
     }
   };
+
+  // V^T operand reads: lane reads 4 columns 32 dt + 16 (G & 1) + 4 m4 .. of
+  // rows 16 kc + 4 (G >> 1) + j4 and that + 8 (the chunk placement does not
+  // depend on kc).
+  int voffr[2][2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int r = 4 * (G >> 1) + j4 + 8 * h2, col = 32 * dt + 16 * (G & 1) + 4 * m4;
+      voffr[dt][h2] = r * HD + 8 * ((col >> 3) ^ sw16(r)) + (col & 7);
+    }
 
   // Transform tile kb's scores (cur) into weights, accumulate P V. Only tiles
   // that cross the diagonal (diag_tag = true_type) evaluate the causal mask.
@@ -243,18 +258,18 @@ __device__ __forceinline__ void fwd_body(
     // key 16kc + 8(s/4) + 4g + s%4 (the accumulator rows the lane owns); the
     // V^T operand is read from the row-major V tile with two transposing
     // reads whose row order matches.
-    const int buf = kb & 1;
+    const bf16* Vt = Vr[kb % 3];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       const int mt = kc >> 1, rr = 8 * (kc & 1);
       bf16x8 pb;
 #pragma unroll
       for (int s = 0; s < 8; ++s) pb[s] = (bf16)cur[mt][rr + s];
-      const int vrow = 16 * kc + 4 * (G >> 1) + j4;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
-        const bf16* vp = &Vs[buf][vrow * VSTR + 32 * dt + 16 * (G & 1) + 4 * m4];
-        oacc[dt] = mfma32(join(read_tr(vp), read_tr(vp + 8 * VSTR)), pb, oacc[dt]);
+        const bf16* vp = &Vt[16 * kc * HD];
+        oacc[dt] = mfma32(join(read_tr(vp + voffr[dt][0]), read_tr(vp + voffr[dt][1])), pb,
+                          oacc[dt]);
       }
     }
   };
@@ -288,18 +303,24 @@ __device__ __forceinline__ void fwd_body(
           consume(std::false_type{}, kb, cur);
       }
     }
-    const int t = my_tile(kb);
-    if (t < nkb) lstore(kloader ? (kb & 1) : ((kb + 1) & 1));
+    // K_{kb+2} and V_{kb+1} (for step kb + 1) are this wave's loads issued
+    // before the last batch, K_{kb+3} and V_{kb+2}.
+    if (kb + 3 < nkb)
+      wait_vmcnt<4>();
+    else if (kb + 2 < nkb)
+      wait_vmcnt<2>();
+    else
+      wait_vmcnt<0>();
     __syncthreads();
-    if (my_tile(kb + 1) < nkb) gload(my_tile(kb + 1));
+    if (kb + 4 < nkb) issue_k(kb + 4);
+    if (kb + 3 < nkb) issue_v(kb + 3);
   };
 
   f32x16 sa[2], sb[2];
   scores(0, sa);
-  // Step 0 refills K buffer 0 (K_2): every wave must have read K_0 first.
-  // Later steps refill a K buffer read one step earlier, before that step's
-  // closing barrier.
-  __syncthreads();
+  __syncthreads();  // every wave has read K_0, whose slot takes K_3
+  if (3 < nkb) issue_k(3);
+  if (2 < nkb) issue_v(2);
   for (int kb = 0; kb < nkb; kb += 2) {
     step(kb, sa, sb);
     if (kb + 1 < nkb) step(kb + 1, sb, sa);
@@ -332,15 +353,15 @@ __global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
     float* __restrict__ stat, int H, int T_, KVariant lo, KVariant hi,
     const int32_t* __restrict__ guard, FwdPrep prep) {
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][FBN * KSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[2][FBN * VSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Kr[3][FBN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 Vr[3][FBN * HD];
   __shared__ float red[3][4];
   if (LO == HI || guard_in_range(guard))
     fwd_body<cfg_mode(LO), cfg_fast(LO), cfg_bounded(LO), cfg_l2n(LO), cfg_poly(LO)>(
-        q, k, v, sink, o, o_precise, stat, H, T_, lo, prep, Ks, Vs, red, blockIdx.x, gridDim.x);
+        q, k, v, sink, o, o_precise, stat, H, T_, lo, prep, Kr, Vr, red, blockIdx.x, gridDim.x);
   else
     fwd_body<cfg_mode(HI), cfg_fast(HI), cfg_bounded(HI), cfg_l2n(HI), cfg_poly(HI)>(
-        q, k, v, sink, o, o_precise, stat, H, T_, hi, prep, Ks, Vs, red, blockIdx.x, gridDim.x);
+        q, k, v, sink, o, o_precise, stat, H, T_, hi, prep, Kr, Vr, red, blockIdx.x, gridDim.x);
 }
 
 // The guard's closing step and the high half of lax.cond in one launch.
@@ -361,8 +382,8 @@ __global__ __launch_bounds__(256, 2) void fwd_fallback_kernel(
     const bf16* __restrict__ q_s, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
     float* __restrict__ stat, int H, int T_, KVariant hi, GuardIn gin, int ntiles) {
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][FBN * KSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[2][FBN * VSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Kr[3][FBN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 Vr[3][FBN * HD];
   __shared__ float red[3][4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   float mx[3] = {0.0f, 0.0f, 0.0f};
@@ -401,7 +422,7 @@ __global__ __launch_bounds__(256, 2) void fwd_fallback_kernel(
   for (int b = blockIdx.x; b < ntiles; b += gridDim.x) {
     __syncthreads();  // LDS of the previous tile is no longer read
     fwd_body<cfg_mode(HI), cfg_fast(HI), cfg_bounded(HI), cfg_l2n(HI), cfg_poly(HI)>(
-        q_s, k, v, sink, o, o_precise, stat, H, T_, hi, FwdPrep{}, Ks, Vs, red, b, ntiles);
+        q_s, k, v, sink, o, o_precise, stat, H, T_, hi, FwdPrep{}, Kr, Vr, red, b, ntiles);
   }
 }
 

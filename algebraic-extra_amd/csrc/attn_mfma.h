@@ -9,8 +9,35 @@ namespace mfma {
 constexpr int HD = 64;
 // forward tiles: 128 queries per workgroup (32 per wave), 64-key tiles
 constexpr int FBM = 128, FBN = 64;
-constexpr int KSTR = 72;  // K tile row stride (bf16): 144 B rows
-constexpr int VSTR = 72;  // V^T tile row stride
+
+// Unpadded [row][64] bf16 tiles (128-byte rows) whose 16-byte chunk c of row
+// r sits at chunk c ^ sw16(r), a bijection of (r / 2) % 8. Sixteen
+// consecutive rows read at one chunk (16-byte reads) and four consecutive
+// rows read over four consecutive chunks (8-byte transposing reads) each
+// touch the 64 LDS banks once.
+__device__ __forceinline__ int sw16(int r) {
+  const int m = (r >> 1) & 7;
+  return ((m & 1) << 2) | (m >> 1);
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ unsigned lds_u32(const void* p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Direct-to-LDS load: lane i's 16 bytes at global `base` + voff land at LDS
+// byte address lds + 16 i (M0 = the wave-uniform lds). Issued as assembly so
+// that the compiler's wait insertion does not treat every later LDS read as
+// depending on it; callers wait for their loads with explicit vmcnt counts.
+__device__ __forceinline__ void dma16_s(const void* base, unsigned voff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N), expcnt/lgkmcnt unconstrained (N < 16).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
 
 enum { MODE_SOFTMAX = 0, MODE_NOSHIFT = 1, MODE_SHIFT = 2 };
 
