@@ -432,6 +432,72 @@ def run_once(which, dev, steps=3):
     torch.cuda.synchronize()
 
 
+def read_sclk_mhz():
+    """Current shader clock of GPU 0 from rocm-smi (None when unavailable)."""
+    import re
+    import subprocess
+    try:
+        out = subprocess.run(["rocm-smi", "--showclocks", "--json"], capture_output=True,
+                             text=True, timeout=5).stdout
+        for card in json.loads(out).values():
+            for key, val in card.items():
+                if "sclk clock speed" in key:
+                    return float(re.sub(r"[^0-9.]", "", str(val)))
+    except Exception:
+        return None
+    return None
+
+
+def bench_clock(dev, seconds=3.0):
+    """The configs[1] attention step (fwd + bwd) back to back for `seconds`,
+    on the benchmark's inputs and on all-zero q, k, v, dO, with the shader
+    clock sampled by rocm-smi meanwhile: under the benchmark's inputs the step
+    runs at the board's power limit, below the maximum clock."""
+    import threading
+    import torch
+    from algebraic_amd.kernels import flash_attention
+    out = {"workload": "configs[1] attention fwd+bwd back to back, rocm-smi shader clock"}
+    for name in ("random", "zero"):
+        q, k, v, do = make_attention_inputs(8, 12, 2048, 64, 1, dev)
+        if name == "zero":
+            with torch.no_grad():
+                for x in (q, k, v, do):
+                    x.zero_()
+
+        def step():
+            o = flash_attention(q, k, v, kind="asinh", n=16, c=8.0, range_guard=True)
+            torch.autograd.grad(o, (q, k, v), do)
+
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+        samples, stop = [], threading.Event()
+
+        def sample():
+            while not stop.is_set():
+                mhz = read_sclk_mhz()
+                if mhz is not None:
+                    samples.append(mhz)
+                time.sleep(0.1)
+
+        th = threading.Thread(target=sample)
+        th.start()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(50):
+                step()
+            n += 50
+            torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / n
+        stop.set()
+        th.join()
+        tail = samples[len(samples) // 2:]  # after the clock has settled
+        out[name] = {"ms_per_step": dt * 1e3,
+                     "sclk_mhz": sum(tail) / len(tail) if tail else None,
+                     "samples": len(samples)}
+    return out
+
+
 def bench_newton_schulz(steps, warmup, dev):
     """Muon's Newton-Schulz at the 350M model's shapes: the 96 [1024, 1024]
     and 72 [1024, 2688] matrices of one training step (optimizers.py:27-65,
@@ -486,6 +552,9 @@ def main():
                     help="print only the 350M model lines (algebraic and standard)")
     ap.add_argument("--elementwise-only", action="store_true",
                     help="print only the rms_norm / alu_glu line")
+    ap.add_argument("--clock", action="store_true",
+                    help="print only the shader-clock line (attention step on random vs zero "
+                         "inputs, rocm-smi sampling)")
     ap.add_argument("--ns-only", action="store_true",
                     help="print only the Newton-Schulz line (Muon at the 350M model's shapes)")
     ap.add_argument("--once", choices=("attn", "attn16", "head", "qknorm"),
@@ -532,6 +601,9 @@ def main():
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
                           for k, v in bench_elementwise(args.steps, args.warmup, dev).items()}),
               flush=True)
+        return
+    if args.clock:
+        print(json.dumps(bench_clock(dev)), flush=True)
         return
     if args.ns_only:
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v)
