@@ -180,7 +180,8 @@ def _ns_native_ok(X: torch.Tensor) -> bool:
 
 
 def _ns_iterate(X: torch.Tensor, steps: int) -> torch.Tensor:
-    """The iteration on a normalised, contiguous batch (k, m, n), m <= n."""
+    """The iteration on a normalised, contiguous batch (k, m, n), m <= n. On
+    the native path X is also a working buffer (overwritten)."""
     return _ns_iterate_many([X], steps)[0]
 
 
@@ -194,7 +195,10 @@ def _ns_iterate_many(Xs_in, steps: int):
     on libalgx's GEMM core, all batches of one product in one launch
     (gemm_bf16_grouped, four at most): X X^T reads X k-contiguous on both
     sides (no transpose is formed), A A and B X read their second operand as
-    [k][n], and every product writes a buffer of its own (no self copy)."""
+    [k][n], and every product writes a buffer of its own (no self copy). The
+    input batches are working buffers of the native path (the iterate
+    ping-pongs between each input and one more buffer of its shape), so their
+    contents are overwritten."""
     a, b, c = _NS_ABC
     if 0 < len(Xs_in) <= 4 and all(_ns_native_ok(X) for X in Xs_in):
         st = []
