@@ -33,8 +33,58 @@ constexpr int BKN = 256;   // keys per workgroup
 constexpr int BQ = 64;     // queries per tile
 constexpr int NWAVE = 8;
 constexpr int NTHR = 64 * NWAVE;
-constexpr int RSTR = 72;   // LDS row stride (bf16) of the Q_s, dO and dS^T tiles
+constexpr int RSTR = 72;   // LDS row stride (bf16) of the Q_s and dO tiles: 144 B
+constexpr int DSTR = 68;   // LDS row stride (bf16) of the dS^T tiles: 136 B
 constexpr int KTR = BKN + 8;  // LDS row stride of K^T [d][key]
+
+// Physical LDS rows. Query row r of a Q_s/dO tile sits at qrow_of(r): the two
+// 2-bit fields of r inside its 16-row block swapped, so the four consecutive
+// rows a transposing read gathers land 16 banks apart (144-byte pitch) while
+// any 16 consecutive rows still cover the banks for 16-byte row reads. Key
+// row r of a dS^T tile sits at krow_of(r), a bit permutation inside its
+// 32-row block that puts the eight rows of one transposing read pass 8 banks
+// apart (136-byte pitch); 32 consecutive rows stay distinct for the 8-byte
+// row stores. Both are fixed permutations, so every access is a per-lane base
+// plus compile-time offsets.
+__host__ __device__ constexpr int qrow_of(int r) {
+  return (r & ~15) | ((r & 3) << 2) | ((r >> 2) & 3);
+}
+__host__ __device__ constexpr int krow_of(int r) {
+  return (r & ~31) | ((r >> 3) & 1) << 4 | (r & 3) << 2 | ((r >> 2) & 1) << 1 | ((r >> 4) & 1);
+}
+// The identities the kernel's addressing uses: both maps are permutations of
+// their blocks (qrow_of an involution, used by the tile loader as its own
+// inverse), and the rows a transposing read gathers, logical 4a + j (+ 8) and
+// 8G + j (+ 4), sit at a per-lane base plus 2.
+constexpr bool row_maps_ok() {
+  bool seen_q[64] = {}, seen_k[256] = {};
+  for (int r = 0; r < 64; ++r) {
+    if (qrow_of(qrow_of(r)) != r || qrow_of(r) >> 4 != r >> 4) return false;
+    seen_q[qrow_of(r)] = true;
+  }
+  for (int r = 0; r < 256; ++r) {
+    if (krow_of(r) >> 5 != r >> 5) return false;
+    seen_k[krow_of(r)] = true;
+  }
+  for (int r = 0; r < 64; ++r)
+    if (!seen_q[r]) return false;
+  for (int r = 0; r < 256; ++r)
+    if (!seen_k[r]) return false;
+  for (int k = 0; k < 4; ++k)
+    for (int a = 0; a < 2; ++a)
+      for (int j = 0; j < 4; ++j)
+        for (int o = 0; o < 2; ++o)
+          if (qrow_of(16 * k + 4 * a + j + 8 * o) != 16 * k + 4 * j + a + 2 * o) return false;
+  for (int kk = 0; kk < 8; ++kk)
+    for (int G = 0; G < 4; ++G)
+      for (int j = 0; j < 4; ++j)
+        for (int o = 0; o < 2; ++o)
+          if (krow_of(32 * kk + 8 * G + j + 4 * o) !=
+              32 * kk + 16 * (G & 1) + 4 * j + (G >> 1) + 2 * o)
+            return false;
+  return true;
+}
+static_assert(row_maps_ok(), "LDS row permutations");
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -66,7 +116,7 @@ struct BwdLds {
   bf16 g[2][BQ * RSTR];     // dO tile
   float st[2][BQ];          // statistic (or its row factor)
   float dd[2][BQ];          // di
-  bf16 dst[2][BKN * RSTR];  // dS^T [key][query]
+  bf16 dst[2][BKN * DSTR];  // dS^T [key][query]
   bf16 kt[HD * KTR];        // K^T of the workgroup [d][key]
 };
 
@@ -117,7 +167,8 @@ __device__ __forceinline__ void bwd_body(
                         : bf16x8{};
 #pragma unroll
     for (int e = 0; e < 8; ++e) L.kt[(col + e) * KTR + row] = val[e];
-    *reinterpret_cast<bf16x8*>(&L.dst[1][row * RSTR + col]) = bf16x8{};
+    *reinterpret_cast<bf16x4*>(&L.dst[1][row * DSTR + col]) = bf16x4{};
+    *reinterpret_cast<bf16x4*>(&L.dst[1][row * DSTR + col + 4]) = bf16x4{};
   }
 
   f32x16 dka[2], dva[2];
@@ -127,8 +178,11 @@ __device__ __forceinline__ void bwd_body(
     zero16(dva[dt]);
   }
 
-  // Tile loader: thread t moves Q_s and dO row t/8, d 8(t%8) .. +7.
-  const int lrow = tid >> 3, lcol = 8 * (tid & 7);
+  // Tile loader: thread t moves d 8(t%8) .. +7 of the Q_s and dO row stored
+  // at physical row prow; the 16 threads of one LDS store pass cover rows 8
+  // apart (32 banks apart).
+  const int prow = 16 * (tid >> 7) + ((tid >> 4) & 7) + 8 * ((tid >> 3) & 1);
+  const int lrow = qrow_of(prow), lcol = 8 * (tid & 7);
   bf16x8 preq, preg;
   float pst = 0.0f, pdi = 0.0f;
   const int qt0 = key0 / BQ, nqt = T_ / BQ;
@@ -142,8 +196,8 @@ __device__ __forceinline__ void bwd_body(
     pdi = di[rbase + qt * BQ + lane];
   };
   auto lstore = [&](int buf) {
-    *reinterpret_cast<bf16x8*>(&L.q[buf][lrow * RSTR + lcol]) = preq;
-    *reinterpret_cast<bf16x8*>(&L.g[buf][lrow * RSTR + lcol]) = preg;
+    *reinterpret_cast<bf16x8*>(&L.q[buf][prow * RSTR + lcol]) = preq;
+    *reinterpret_cast<bf16x8*>(&L.g[buf][prow * RSTR + lcol]) = preg;
     L.st[buf][lane] = stat_pow ? powN<L2N>(pst, log2n) : pst;
     L.dd[buf][lane] = pdi;
   };
@@ -152,8 +206,8 @@ __device__ __forceinline__ void bwd_body(
   auto half_scores = [&](int buf, int mq, f32x16& s, f32x16& dp) {
     zero16(s);
     zero16(dp);
-    const bf16* qrow = &L.q[buf][(32 * mq + c32) * RSTR + 8 * g];
-    const bf16* grow = &L.g[buf][(32 * mq + c32) * RSTR + 8 * g];
+    const bf16* qrow = &L.q[buf][(32 * mq + qrow_of(c32)) * RSTR + 8 * g];
+    const bf16* grow = &L.g[buf][(32 * mq + qrow_of(c32)) * RSTR + 8 * g];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       s = mfma32(*reinterpret_cast<const bf16x8*>(qrow + 16 * ks), kreg[ks], s);
@@ -194,19 +248,20 @@ __device__ __forceinline__ void bwd_body(
   auto half_update = [&](int buf, int mq, const bf16x8 (&pb)[2], const bf16x8 (&db)[2]) {
 #pragma unroll
     for (int kcl = 0; kcl < 2; ++kcl) {
-      const int qbase = 16 * (2 * mq + kcl) + 4 * (G >> 1) + j4;
+      // Physical rows of queries 16(2mq + kcl) + 4(G >> 1) + j4 (+ 8).
+      const int qbase = 16 * (2 * mq + kcl) + 4 * j4 + (G >> 1);
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
         const int col = 32 * dt + 16 * (G & 1) + 4 * m4;
         const bf16x8 ag = join(read_tr(&L.g[buf][qbase * RSTR + col]),
-                               read_tr(&L.g[buf][(qbase + 8) * RSTR + col]));
+                               read_tr(&L.g[buf][(qbase + 2) * RSTR + col]));
         const bf16x8 aq = join(read_tr(&L.q[buf][qbase * RSTR + col]),
-                               read_tr(&L.q[buf][(qbase + 8) * RSTR + col]));
+                               read_tr(&L.q[buf][(qbase + 2) * RSTR + col]));
         dva[dt] = mfma32(ag, pb[kcl], dva[dt]);
         dka[dt] = mfma32(aq, db[kcl], dka[dt]);
       }
     }
-    bf16* drow = &L.dst[buf][(32 * w + c32) * RSTR + 32 * mq + 4 * g];
+    bf16* drow = &L.dst[buf][(32 * w + krow_of(c32)) * DSTR + 32 * mq + 4 * g];
 #pragma unroll
     for (int kcl = 0; kcl < 2; ++kcl) {
       *reinterpret_cast<bf16x4*>(drow + 16 * kcl) =
@@ -216,7 +271,7 @@ __device__ __forceinline__ void bwd_body(
     }
   };
   auto zero_dst = [&](int buf) {
-    bf16* drow = &L.dst[buf][(32 * w + c32) * RSTR + 4 * g];
+    bf16* drow = &L.dst[buf][(32 * w + krow_of(c32)) * DSTR + 4 * g];
 #pragma unroll
     for (int j = 0; j < 8; ++j) *reinterpret_cast<bf16x4*>(drow + 8 * j) = bf16x4{};
   };
@@ -227,9 +282,10 @@ __device__ __forceinline__ void bwd_body(
     f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
 #pragma unroll
     for (int kk = 0; kk < BKN / 32; ++kk) {
-      const int krow = 32 * kk + 8 * G + j4;
-      const bf16x8 a = join(read_tr(&L.dst[buf][krow * RSTR + qr + 4 * m4]),
-                            read_tr(&L.dst[buf][(krow + 4) * RSTR + qr + 4 * m4]));
+      // Physical rows of keys 32kk + 8G + j4 (+ 4).
+      const int krow = 32 * kk + 16 * (G & 1) + 4 * j4 + (G >> 1);
+      const bf16x8 a = join(read_tr(&L.dst[buf][krow * DSTR + qr + 4 * m4]),
+                            read_tr(&L.dst[buf][(krow + 2) * DSTR + qr + 4 * m4]));
       const bf16* kcol = &L.kt[(dc + i16) * KTR + 32 * kk + 8 * G];
       const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(kcol);
       const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(kcol + 16 * KTR);

@@ -449,17 +449,20 @@ def read_sclk_mhz():
 
 
 def bench_clock(dev, seconds=3.0):
-    """The configs[1] attention step (fwd + bwd) back to back for `seconds`,
-    on the benchmark's inputs and on all-zero q, k, v, dO, with the shader
-    clock sampled by rocm-smi meanwhile: under the benchmark's inputs the step
-    runs at the board's power limit, below the maximum clock."""
+    """Hot-path steps run back to back for `seconds` each while rocm-smi
+    samples the shader clock: the configs[1] attention step (fwd + bwd) and
+    the configs[2] fused-head step (forward statistics, dz, dh + dE), each on
+    the benchmark's inputs and on all-zero inputs, and the library's plain
+    GEMM of the head's logits shape beside them. Under the benchmark's inputs
+    these steps run at the board's power limit, below the maximum clock, and
+    the clock depends on the data the MFMAs multiply."""
     import threading
     import torch
-    from algebraic_amd.kernels import flash_attention
-    out = {"workload": "configs[1] attention fwd+bwd back to back, rocm-smi shader clock"}
-    for name in ("random", "zero"):
+    from algebraic_amd.kernels import flash_attention, fused_head
+
+    def attention(zero):
         q, k, v, do = make_attention_inputs(8, 12, 2048, 64, 1, dev)
-        if name == "zero":
+        if zero:
             with torch.no_grad():
                 for x in (q, k, v, do):
                     x.zero_()
@@ -467,8 +470,41 @@ def bench_clock(dev, seconds=3.0):
         def step():
             o = flash_attention(q, k, v, kind="asinh", n=16, c=8.0, range_guard=True)
             torch.autograd.grad(o, (q, k, v), do)
+        return step
 
-        for _ in range(10):
+    def head(zero):
+        gen = torch.Generator(device=dev).manual_seed(2)
+        N, d, V = 16384, 768, 50304
+        h = torch.randn((N, d), device=dev, generator=gen).bfloat16()
+        E = (torch.randn((V, d), device=dev, generator=gen) * 0.02).bfloat16()
+        if zero:
+            h.zero_()
+            E.zero_()
+        h.requires_grad_(True)
+        E.requires_grad_(True)
+        t = torch.randint(0, V, (N,), device=dev, generator=gen, dtype=torch.int64)
+
+        def step():
+            obj, _ = fused_head(h, E, t, kind="alg_ce", n=8, c=2.0)
+            torch.autograd.grad(obj, (h, E))
+        return step
+
+    def library_logits():
+        gen = torch.Generator(device=dev).manual_seed(2)
+        h = torch.randn((16384, 768), device=dev, generator=gen).bfloat16()
+        E = (torch.randn((50304, 768), device=dev, generator=gen) * 0.02).bfloat16()
+        return lambda: torch.mm(h, E.t())
+
+    cases = {"attention_random": (lambda: attention(False), 50),
+             "attention_zero": (lambda: attention(True), 50),
+             "head_random": (lambda: head(False), 5),
+             "head_zero": (lambda: head(True), 5),
+             "library_logits_gemm_random": (library_logits, 5)}
+    out = {"workload": "configs[1] attention fwd+bwd, configs[2] fused-head fwd+bwd and the "
+                       "library GEMM h E^T, each back to back; rocm-smi shader clock"}
+    for name, (make, batch) in cases.items():
+        step = make()
+        for _ in range(2 * batch):
             step()
         torch.cuda.synchronize()
         samples, stop = [], threading.Event()
@@ -484,17 +520,20 @@ def bench_clock(dev, seconds=3.0):
         th.start()
         n, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < seconds:
-            for _ in range(50):
+            for _ in range(batch):
                 step()
-            n += 50
+            n += batch
             torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / n
         stop.set()
         th.join()
         tail = samples[len(samples) // 2:]  # after the clock has settled
-        out[name] = {"ms_per_step": dt * 1e3,
-                     "sclk_mhz": sum(tail) / len(tail) if tail else None,
+        out[name] = {"ms_per_step": round(dt * 1e3, 4),
+                     "sclk_mhz": round(sum(tail) / len(tail), 1) if tail else None,
                      "samples": len(samples)}
+        print(json.dumps({name: out[name]}), flush=True)
+        del step
+        torch.cuda.empty_cache()
     return out
 
 
