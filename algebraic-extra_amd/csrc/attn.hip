@@ -5,6 +5,7 @@
 // grid; the generic path enqueues both variants and the unselected one
 // returns at once. Either way this mirrors lax.cond(in_range, low, high) of
 // flash.py:853-856 without a host round trip.
+#include <initializer_list>
 #include <cstdlib>
 #include <mutex>
 
@@ -70,6 +71,14 @@ bool force_generic() {
   return e != nullptr && e[0] == '1';
 }
 
+// The kernels move (B, H, T, D) rows with 16-byte vector accesses.
+int32_t check_aligned(const char* who, std::initializer_list<const void*> ptrs) {
+  for (const void* p : ptrs)
+    if (p != nullptr && (reinterpret_cast<uintptr_t>(p) & 15) != 0)
+      return fail(std::string(who) + ": q, k, v, o, dO and gradient tensors must be 16-byte aligned");
+  return 0;
+}
+
 int32_t check_shape(int B, int H, int T, int D, int dtype) {
   if (B < 0 || H < 0 || T < 0) return fail("attn: negative size");
   if (dtype != ALGX_BF16 && dtype != ALGX_F32) return fail("attn: dtype must be bf16 or f32");
@@ -93,6 +102,7 @@ extern "C" int32_t algx_attn_prepare(const void* q, const void* k, const void* v
   if (q == nullptr || q_s == nullptr) return fail("attn_prepare: null q or q_s");
   if (guard != nullptr && (k == nullptr || v == nullptr))
     return fail("attn_prepare: the guard needs k and v");
+  if (int32_t rc = check_aligned("attn_prepare", {q, k, v, q_s})) return rc;
   return launch_prepare(q, k, v, sink, q_s, guard, B, H, T, D, dtype, q_scale, bound, vmax,
                         (hipStream_t)stream);
 }
@@ -115,6 +125,7 @@ extern "C" int32_t algx_attn_fwd(const void* q, const void* k, const void* v, co
     return fail("attn_fwd: null pointer");
   if ((kl.precise || (guard != nullptr && kh.precise)) && o_precise == nullptr)
     return fail("attn_fwd: precise-output variant needs o_precise");
+  if (int32_t rc = check_aligned("attn_fwd", {q, k, v, o, o_precise})) return rc;
   hipStream_t s = (hipStream_t)stream;
   if (mfma_supported(T, D, dtype) && !force_generic())
     return launch_fwd_mfma(q, k, v, sink, o, o_precise, stat, B, H, T, kl, kh, guard, s);
@@ -155,6 +166,7 @@ extern "C" int32_t algx_attn_forward(const void* q, const void* k, const void* v
     return fail("attn_forward: null pointer");
   if ((kl.precise || (guard != nullptr && kh.precise)) && o_precise == nullptr)
     return fail("attn_forward: precise-output variant needs o_precise");
+  if (int32_t rc = check_aligned("attn_forward", {q, k, v, q_s, o, o_precise})) return rc;
   hipStream_t s = (hipStream_t)stream;
   if (mfma_supported(T, D, dtype) && !force_generic()) {
     if (guard != nullptr && workspace == nullptr)
@@ -207,6 +219,8 @@ extern "C" int32_t algx_attn_bwd(const void* q, const void* k, const void* v, co
     return fail("attn_bwd: null pointer");
   if ((kl.precise || kh.precise) && o_precise == nullptr)
     return fail("attn_bwd: precise-output variant needs o_precise");
+  if (int32_t rc = check_aligned("attn_bwd", {q, k, v, o, o_precise, dout, dq, dk, dv, workspace}))
+    return rc;
   const bool mfma = mfma_supported(T, D, dtype) && !force_generic();
   float* dq_acc = (float*)workspace;
   float* di = (float*)((char*)workspace + rows * D * (int64_t)sizeof(float));

@@ -108,7 +108,10 @@ int32_t algx_qknorm_pair_bwd(const void* xq, const void* xk, const float* gain_q
  * head_resident.forward head_resident.py:138-155) and the custom VJP
  * (_flash_bwd :718-726, _backward :630-687, head_resident.backward :158-176).
  *
- * q, q_s, k, v, o, dout, dq, dk, dv: (B, H, T, D) in `dtype`. sink: (H,)
+ * q, q_s, k, v, o, dout, dq, dk, dv: (B, H, T, D) in `dtype`, contiguous and
+ * 16-byte aligned, as are o_precise and the backward workspace (the kernels
+ * move rows with 16-byte vector accesses; a misaligned pointer is rejected
+ * with an error before any launch). sink: (H,)
  * float32 in kernel units (sink_logit / c), or NULL. stat: (B, H, T) float32.
  *
  * algx_attn_prepare forms the pre-scaled query q_s = cast(q * q_scale)

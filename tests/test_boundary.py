@@ -75,6 +75,21 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     rc = lib.algx_alu_glu_fwd(ctypes.c_void_p(16), ctypes.c_void_p(24), ctypes.c_void_p(32), 16, 0,
                               1.0, None)
     assert rc != 0 and b"16-byte aligned" in lib.algx_last_error()
+    # Attention tensors: a pointer that is not 16-byte aligned (here o) is
+    # rejected before any launch, on every entry point.
+    v = _lib.AttnVariant(kind=1, n=16)
+    a, bad = ctypes.c_void_p(256), ctypes.c_void_p(264)
+    rc = lib.algx_attn_fwd(a, a, a, None, bad, None, a, 1, 1, 128, 64, 0, v, None, None, None)
+    assert rc != 0 and b"attn_fwd" in lib.algx_last_error()
+    assert b"16-byte aligned" in lib.algx_last_error()
+    rc = lib.algx_attn_forward(a, a, a, None, a, bad, None, a, None, None, 1, 1, 128, 64, 0,
+                               1.0, 1.0, 1.0, v, None, None)
+    assert rc != 0 and b"attn_forward: q, k, v" in lib.algx_last_error()
+    rc = lib.algx_attn_bwd(a, a, a, None, a, None, a, a, bad, a, a, None, a, 1, 1, 128, 64, 0,
+                           1.0, v, None, None, None)
+    assert rc != 0 and b"attn_bwd: q, k, v" in lib.algx_last_error()
+    rc = lib.algx_attn_prepare(a, a, a, None, bad, None, 1, 1, 128, 64, 0, 1.0, 1.0, 1.0, None)
+    assert rc != 0 and b"attn_prepare: q, k, v" in lib.algx_last_error()
 
 
 def test_grouped_gemm_validation_without_a_gpu():
