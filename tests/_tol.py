@@ -15,6 +15,10 @@ F32_RTOL = 1e-4
 BF16_MAX_ABS = 2e-2
 BF16_REL_L2 = 1e-2
 
+# Every bf16 comparison of the session: (what, max-abs error, max|b|, rel-L2),
+# so the unscaled max-abs against the fixed 2e-2 can be reported at the end.
+BF16_RECORDS = []
+
 
 def to_np(t):
     import torch
@@ -45,6 +49,7 @@ def assert_bf16(got, want, max_abs=BF16_MAX_ABS, rel=BF16_REL_L2, what=""):
     mae = float(np.abs(a - b).max()) if a.size else 0.0
     bound = max_abs * max(1.0, float(np.abs(b).max()) if b.size else 1.0)
     r = rel_l2(a, b)
+    BF16_RECORDS.append((what, mae, float(np.abs(b).max()) if b.size else 0.0, r))
     assert mae <= bound and r <= rel, f"{what}: max-abs {mae:.3e} (<= {bound:.3e}), rel-L2 {r:.3e} (<= {rel})"
 
 
