@@ -377,19 +377,26 @@ __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t s
     const bf16 *na0 = sa0, *na1 = sa1, *nb0 = sb0, *nb1 = sb1;
     if (t + 1 < ntiles) src(t + 1, na0, na1, nb0, nb1);
     const int g0 = t * nk;
-    auto step = [&](int kk, const bf16* cur, const bf16* nxt, bf16* refill) {
+    // `synced`: this stage's wait, barrier and refill already ran before the
+    // previous tile's epilogue (the first stage of every tile but the first);
+    // `landed`: this wave's loads of the stage it waits for are known to have
+    // landed (the second stage of such a tile), so only the barrier remains.
+    auto step = [&](int kk, const bf16* cur, const bf16* nxt, bf16* refill, bool synced,
+                    bool landed) {
       rd(cur, 1, ya, yb);
       __builtin_amdgcn_sched_barrier(0);
       mm(xa, xb);
       __builtin_amdgcn_sched_barrier(0);
-      // Wait for stage g + 1; the stages issued after it may stay in flight.
-      const int g = g0 + kk;
-      wait_stages(min(g + S - 2, G - 1) - (g + 1));
-      asm volatile("s_barrier" ::: "memory");
-      if (kk + S - 1 < nk)
-        issue(sa0, sa1, sb0, sb1, kk + S - 1, refill);
-      else if (t + 1 < ntiles)
-        issue(na0, na1, nb0, nb1, kk + S - 1 - nk, refill);
+      if (!synced) {
+        // Wait for stage g + 1; the stages issued after it may stay in flight.
+        const int g = g0 + kk;
+        if (!landed) wait_stages(min(g + S - 2, G - 1) - (g + 1));
+        asm volatile("s_barrier" ::: "memory");
+        if (kk + S - 1 < nk)
+          issue(sa0, sa1, sb0, sb1, kk + S - 1, refill);
+        else if (t + 1 < ntiles)
+          issue(na0, na1, nb0, nb1, kk + S - 1 - nk, refill);
+      }
       rd(nxt, 0, xa, xb);
       __builtin_amdgcn_sched_barrier(0);
       mm(ya, yb);
@@ -399,7 +406,24 @@ __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t s
 #pragma unroll
       for (int u = 0; u < S; ++u)
         if (kk + u < nk)
-          step(kk + u, ring.slot[u], ring.slot[(u + 1) % S], ring.slot[(u + S - 1) % S]);
+          step(kk + u, ring.slot[u], ring.slot[(u + 1) % S], ring.slot[(u + S - 1) % S],
+               u == 0 && kk == 0 && t > 0, S >= 4 && u == 1 && kk == 0 && t > 0);
+    }
+    if (t + 1 < ntiles) {
+      // Global stores count in vmcnt, and the loads and stores of one wave
+      // are not known to retire in order, so a vmcnt wait only bounds the
+      // loads still in flight. A wait issued after this tile's epilogue stores
+      // would therefore also wait for them to land. So the next tile's first
+      // wait, barrier and refill (stage S - 1 of that tile; nk >= S here) run
+      // before the epilogue, and so does the wait for the next tile's stage 2
+      // (with S >= 4: only stage S - 1 may stay in flight), which the second
+      // stage would otherwise wait for. The stores then have two stages of
+      // MFMA work before a wait can meet them.
+      const int g = g0 + nk;
+      wait_stages(min(g + S - 2, G - 1) - (g + 1));
+      asm volatile("s_barrier" ::: "memory");
+      issue(na0, na1, nb0, nb1, S - 1, ring.slot[S - 1]);
+      if (S >= 4) wait_vm<4>();
     }
     epi(t, acc);
     acc.zero();
