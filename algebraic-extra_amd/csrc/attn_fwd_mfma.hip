@@ -48,6 +48,10 @@ __device__ __forceinline__ void fwd_body(
     for (int ks = 0; ks < 4; ++ks)
       qreg[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks);
   }
+  // The pre-scale's q_s and the guard's partial maxima are stored at the end
+  // of the kernel: a store issued before the K/V prologue would make its
+  // vmcnt wait also wait for the store to land.
+  float part_out = 0.0f;
   if (prep.q_s != nullptr) {
     // Fused pre-scale: `q` is the raw query; q_s = cast(q * scale)
     // (flash.py:833) is formed in registers and written once for the
@@ -55,7 +59,6 @@ __device__ __forceinline__ void fwd_body(
     // guard's maxima (flash.py:841-849): |q_s|^2 over its 128 query rows and
     // |k|^2, |v| over the 128 key rows of its diagonal block, so the grid
     // covers every row once. NaN becomes +inf so that it fails the guard.
-    bf16* qsp = prep.q_s + base + (int64_t)qrow * HD + 8 * g;
     float sq = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -67,7 +70,6 @@ __device__ __forceinline__ void fwd_body(
         sq = __builtin_fmaf(f, f, sq);
       }
       qreg[ks] = x;
-      *reinterpret_cast<bf16x8*>(qsp + 16 * ks) = x;
     }
     if (prep.partial != nullptr) {
       auto nan_to_inf = [](float x) { return x != x ? __builtin_inff() : x; };
@@ -99,9 +101,8 @@ __device__ __forceinline__ void fwd_body(
       }
       __syncthreads();
       if (tid < 3)
-        prep.partial[(int64_t)bid * 3 + tid] =
-            __builtin_fmaxf(__builtin_fmaxf(red[tid][0], red[tid][1]),
-                            __builtin_fmaxf(red[tid][2], red[tid][3]));
+        part_out = __builtin_fmaxf(__builtin_fmaxf(red[tid][0], red[tid][1]),
+                                   __builtin_fmaxf(red[tid][2], red[tid][3]));
     }
   }
 
@@ -343,6 +344,12 @@ __device__ __forceinline__ void fwd_body(
         *reinterpret_cast<f32x4*>(o_precise + orow + d) = val;
     }
   if (g == 0) stat[(int64_t)bh * T_ + qrow] = final_stat(var, m_row, l_tot);
+  if (prep.q_s != nullptr) {
+    bf16* qsp = prep.q_s + base + (int64_t)qrow * HD + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) *reinterpret_cast<bf16x8*>(qsp + 16 * ks) = qreg[ks];
+    if (prep.partial != nullptr && tid < 3) prep.partial[(int64_t)bid * 3 + tid] = part_out;
+  }
 }
 
 // The guard word (if any) picks the low or the high variant for the whole
