@@ -687,6 +687,10 @@ def main():
     if not args.no_secondary:
         a16 = bench_attention(8, 16, T, D, max(5, args.steps // 2), 2, dev)
         asm = bench_attention(B, H, T, D, max(5, args.steps // 2), 2, dev, kind="softmax")
+        # The memory-bound lines run before the head, whose step and library
+        # comparison allocate ~5 GB (the 1.65 GB dz among them).
+        qk = bench_qknorm(20, 3, dev)
+        ew = bench_elementwise(20, 3, dev)
         line["secondary"] = {
             "attn_h16": {"workload": "configs[3] attention B=8,H=16,T=2048,D=64",
                          "ms_per_step": round(a16["ms_per_step"], 4),
@@ -699,10 +703,9 @@ def main():
                              "frac": round(asm["tflops"] / PEAK_BF16_TFLOPS, 4)},
             "fused_head": {k: (round(v, 4) if isinstance(v, float) else v)
                            for k, v in bench_head(5, 2, dev).items()},
-            "qknorm": {k: (round(v, 4) if isinstance(v, float) else v)
-                       for k, v in bench_qknorm(20, 3, dev).items()},
+            "qknorm": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in qk.items()},
             "elementwise": {k: (round(v, 4) if isinstance(v, float) else v)
-                            for k, v in bench_elementwise(20, 3, dev).items()},
+                            for k, v in ew.items()},
             "newton_schulz": {k: (round(v, 4) if isinstance(v, float) else v)
                               for k, v in bench_newton_schulz(5, 2, dev).items()},
         }
