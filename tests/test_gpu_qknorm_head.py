@@ -125,11 +125,14 @@ def test_fused_head_matches_oracle(kind, n, c, V):
         assert cos > 0.999
 
 
-@pytest.mark.parametrize("N,d,V", [(300, 64, 1000), (600, 40, 257), (8, 128, 300)])
+@pytest.mark.parametrize("N,d,V", [(300, 64, 1000), (600, 40, 257), (8, 128, 300),
+                                   (2048, 128, 16284)])
 def test_fused_head_ragged_tiles(N, d, V):
     """Token counts and vocabularies that leave partial 256-token and
     vocabulary tiles, and a hidden width that is not a multiple of the 32-wide
-    k stage (block_n = N, so the reference's divisibility check holds)."""
+    k stage (block_n = N, so the reference's divisibility check holds). The
+    last case streams two vocabulary tiles of exactly four k stages per
+    workgroup (d = 128) through the direct-to-LDS ring, the last one ragged."""
     h, e, t = _head_inputs(N, d, V, 5, 0.2)
     for kind, n, c in (("alg_ce", 8, 2.0), ("ce", 16, 16.0)):
         got = _head_run(h, e, t, kind=kind, n=n, c=c, block_n=N)
