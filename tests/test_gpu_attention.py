@@ -332,14 +332,16 @@ def test_fused_forward_equals_prepare_then_forward(tail):
 _GRAD_HEADS = ((0, 3), (2, 5), (6, 7))
 
 
+@pytest.mark.parametrize("with_sink", [False, True])
 @pytest.mark.parametrize("H", [12, 16])
-def test_benchmark_shape_backward_selected_heads(H):
+def test_benchmark_shape_backward_selected_heads(H, with_sink):
     """The whole (8, H, 2048, 64) bf16 guarded grid runs forward and backward
     (768 or 1024 backward workgroups, the float32 dQ atomics, the XCD head
     map), with dO nonzero in three heads on different XCD slots: those heads'
-    o, dq, dk, dv match the oracle and every other head's gradients are
-    exactly zero. With dO dense instead, sum_keys dV = sum_queries dO for every
-    (b, h, d) (the weights of each query row sum to one)."""
+    o, dq, dk, dv (and, with a per-head sink, dsink) match the oracle and
+    every other head's gradients are exactly zero. Without a sink and with dO
+    dense instead, sum_keys dV = sum_queries dO for every (b, h, d) (the
+    weights of each query row sum to one)."""
     B, T, D = 8, 2048, 64
     shape = (B, H, T, D)
     gen = torch.Generator(device=DEV).manual_seed(11)
@@ -356,22 +358,35 @@ def test_benchmark_shape_backward_selected_heads(H):
         do[b, h] = do_full[b, h]
     kw = dict(kind="asinh", n=16, c=8.0, range_guard=True)
     tq, tk, tv = (x.clone().requires_grad_(True) for x in (q, k, v))
-    o = flash_attention(tq, tk, tv, **kw)
-    dq, dk, dv = torch.autograd.grad(o, (tq, tk, tv), do)
+    ts = None
+    if with_sink:
+        ts = (0.5 * torch.randn(H, device=DEV, generator=gen)).requires_grad_(True)
+    o = flash_attention(tq, tk, tv, ts, **kw)
+    grads = torch.autograd.grad(o, (tq, tk, tv) + ((ts,) if with_sink else ()), do)
+    dq, dk, dv = grads[:3]
     torch.cuda.synchronize()
     mask = torch.ones((B, H), dtype=torch.bool)
     for b, h in heads:
         mask[b, h] = False
     for name, g in (("dq", dq), ("dk", dk), ("dv", dv)):
         assert torch.count_nonzero(g[mask.to(DEV)]) == 0, name
+    if with_sink:
+        dsink = to_np(grads[3])
+        others = [h for h in range(H) if h not in {hh for _, hh in heads}]
+        assert np.count_nonzero(dsink[others]) == 0
     for b, h in heads:
         sl = (slice(b, b + 1), slice(h, h + 1))
-        res = OA.flash_attention(to_np(q[sl]), to_np(k[sl]), to_np(v[sl]), None, dtype="bf16",
+        res = OA.flash_attention(to_np(q[sl]), to_np(k[sl]), to_np(v[sl]),
+                                 to_np(ts[h:h + 1]) if with_sink else None, dtype="bf16",
                                  do=to_np(do[sl]), **kw)
         assert res.in_range
         assert_bf16(o[sl], res.o, what=f"o{b, h}")
         for got, want, name in zip((dq, dk, dv), res.grads[:3], ("dq", "dk", "dv")):
             assert_bf16(got[sl], want, what=f"{name}{b, h}")
+        if with_sink:
+            assert rel_l2(dsink[h:h + 1], res.grads[3]) <= 1e-2, (h, dsink[h], res.grads[3])
+    if with_sink:
+        return
     # dense dO: column sums of dV equal those of dO, head by head
     dv_full = torch.autograd.grad(flash_attention(tq, tk, tv, **kw), tv, do_full)[0]
     lhs = dv_full.double().sum(2)
