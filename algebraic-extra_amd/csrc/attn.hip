@@ -34,6 +34,11 @@ int32_t to_kvar(const algx_attn_variant* v, KVariant& out, const char* which) {
   out.poly = v->kind == ALGX_ASINH && v->poly_rho != 0;
   if (out.poly && (out.shift || v->n != 16))
     return fail("attn: bounded radical approximation requires shift=False and n=16");
+  // The guard's unclamped low variant is never paired with the polynomial
+  // (flash.py:835-836 refuses range_guard with poly_rho).
+  if (out.poly && out.bounded)
+    return fail("attn: bounded radical approximation requires bounded_scores=0 "
+                "(range_guard is for exact radical evaluation)");
   return 0;
 }
 
@@ -252,12 +257,17 @@ extern "C" int32_t algx_attn_forward_noalloc(const void* q, const void* k, const
                                              float vmax, const algx_attn_variant* low,
                                              const algx_attn_variant* high, void* stream) {
   if (int32_t rc = check_shape(B, H, T, D, dtype)) return rc;
+  // The limit is checked for every guarded call, whichever path would run,
+  // before anything touches the device.
+  if (guard != nullptr && fwd_fused_partials(B, H, T) > kNoAllocParts)
+    return fail("attn_forward_noalloc: B * H * T / 128 exceeds the scratch limit of 65536 "
+                "forward workgroups; use algx_attn_forward with a workspace");
+  if ((int64_t)B * H * T > 0 && (q == nullptr || k == nullptr || v == nullptr ||
+                                 q_s == nullptr || o == nullptr || stat == nullptr))
+    return fail("attn_forward_noalloc: null pointer");
   float* part = nullptr;
   if (guard != nullptr && (int64_t)B * H * T > 0 && mfma_supported(T, D, dtype) &&
       !force_generic()) {
-    if (fwd_fused_partials(B, H, T) > kNoAllocParts)
-      return fail("attn_forward_noalloc: B * H * T / 128 exceeds the scratch limit of 65536 "
-                  "forward workgroups; use algx_attn_forward with a workspace");
     if (int32_t rc = scratch_on_current_device(&part)) return rc;
   }
   return algx_attn_forward(q, k, v, sink, q_s, o, o_precise, stat, guard, part, B, H, T, D,

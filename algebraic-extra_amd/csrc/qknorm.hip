@@ -23,6 +23,7 @@ namespace {
 constexpr int kD = 64;
 constexpr int kThreads = 256;
 constexpr int kMaxBlocks = 2048;
+constexpr int kUnroll = 2;  // rows per lane group in flight per loop iteration
 
 template <typename T> struct Vec;
 template <> struct Vec<bf16> { typedef bf16x8 type; static constexpr int n = 8; };
@@ -62,21 +63,33 @@ __global__ __launch_bounds__(kThreads) void qknorm_fwd_kernel(NormPair<T> P, int
   for (int i = 0; i < EPL; ++i) g[i] = P.gain[t][sub * EPL + i];
   const int64_t wave = (int64_t)blk * (kThreads / 64) + (threadIdx.x >> 6);
   const int64_t stride = (int64_t)nblk * (kThreads / 64) * RPW;
-  for (int64_t row = wave * RPW + rw; row < rows; row += stride) {
-    VT in = *reinterpret_cast<const VT*>(x + row * kD + sub * EPL);
-    float xs[EPL];
-    float ss = 0.0f;
+  // kUnroll rows per lane group and iteration, all loads issued first. A row
+  // past the end reads row 0 and is not stored; the LPR lanes of a group
+  // share a row, so the group shuffles never see a divergent lane.
+  for (int64_t row0 = wave * RPW + rw; row0 < rows; row0 += kUnroll * stride) {
+    VT in[kUnroll];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      xs[i] = to_f(in[i]);
-      ss = __builtin_fmaf(xs[i], xs[i], ss);
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t row = row0 + u * stride;
+      in[u] = *reinterpret_cast<const VT*>(x + (row < rows ? row : 0) * kD + sub * EPL);
     }
-    ss = group_sum<LPR>(ss);
-    const float tau = rsq(ss * (1.0f / kD) + eps);
-    VT out;
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) out[i] = from_f<T>((xs[i] * tau) * g[i]);
-    *reinterpret_cast<VT*>(y + row * kD + sub * EPL) = out;
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t row = row0 + u * stride;
+      float xs[EPL];
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        xs[i] = to_f(in[u][i]);
+        ss = __builtin_fmaf(xs[i], xs[i], ss);
+      }
+      ss = group_sum<LPR>(ss);
+      const float tau = rsq(ss * (1.0f / kD) + eps);
+      VT out;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) out[i] = from_f<T>((xs[i] * tau) * g[i]);
+      if (row < rows) *reinterpret_cast<VT*>(y + row * kD + sub * EPL) = out;
+    }
   }
 }
 
@@ -103,29 +116,42 @@ __global__ __launch_bounds__(kThreads) void qknorm_bwd_kernel(NormPair<T> P,
   }
   const int64_t wave = (int64_t)blk * (kThreads / 64) + (threadIdx.x >> 6);
   const int64_t stride = (int64_t)nblk * (kThreads / 64) * RPW;
-  for (int64_t row = wave * RPW + rw; row < rows; row += stride) {
-    VT xin = *reinterpret_cast<const VT*>(x + row * kD + sub * EPL);
-    VT din = *reinterpret_cast<const VT*>(dy + row * kD + sub * EPL);
-    float xs[EPL], ds[EPL];
-    float ss = 0.0f, dot = 0.0f;
+  // As the forward: kUnroll rows per iteration, loads first; a row past the
+  // end reads row 0, adds nothing to dgain and is not stored.
+  for (int64_t row0 = wave * RPW + rw; row0 < rows; row0 += kUnroll * stride) {
+    VT xin[kUnroll], din[kUnroll];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      xs[i] = to_f(xin[i]);
-      ds[i] = to_f(din[i]);
-      ss = __builtin_fmaf(xs[i], xs[i], ss);
-      dot = __builtin_fmaf(ds[i] * g[i], xs[i], dot);
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t row = row0 + u * stride;
+      const int64_t off = (row < rows ? row : 0) * kD + sub * EPL;
+      xin[u] = *reinterpret_cast<const VT*>(x + off);
+      din[u] = *reinterpret_cast<const VT*>(dy + off);
     }
-    ss = group_sum<LPR>(ss);
-    dot = group_sum<LPR>(dot);
-    const float tau = rsq(ss * (1.0f / kD) + eps);
-    const float c = tau * tau * tau * dot * (1.0f / kD);
-    VT out;
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      out[i] = from_f<T>(tau * g[i] * ds[i] - c * xs[i]);
-      dg[i] = __builtin_fmaf(ds[i], xs[i] * tau, dg[i]);
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t row = row0 + u * stride;
+      const bool live = row < rows;
+      float xs[EPL], ds[EPL];
+      float ss = 0.0f, dot = 0.0f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        xs[i] = to_f(xin[u][i]);
+        ds[i] = live ? to_f(din[u][i]) : 0.0f;
+        ss = __builtin_fmaf(xs[i], xs[i], ss);
+        dot = __builtin_fmaf(ds[i] * g[i], xs[i], dot);
+      }
+      ss = group_sum<LPR>(ss);
+      dot = group_sum<LPR>(dot);
+      const float tau = rsq(ss * (1.0f / kD) + eps);
+      const float c = tau * tau * tau * dot * (1.0f / kD);
+      VT out;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        out[i] = from_f<T>(tau * g[i] * ds[i] - c * xs[i]);
+        dg[i] = __builtin_fmaf(ds[i], xs[i] * tau, dg[i]);
+      }
+      if (live) *reinterpret_cast<VT*>(dx + row * kD + sub * EPL) = out;
     }
-    *reinterpret_cast<VT*>(dx + row * kD + sub * EPL) = out;
   }
   // Reduce dg over the row groups of the wave, then over the block's waves.
   __shared__ float red[kThreads / 64][kD];

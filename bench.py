@@ -43,13 +43,18 @@ def attn_flops_fwd(B, H, T, D):
     return 4.0 * B * H * T * T * D / 2.0      # causal, bench_attention.py:50
 
 
-def make_attention_inputs(B, H, T, D, seed, dev):
+def make_attention_inputs(B, H, T, D, seed, dev, qk_norm=True):
+    """q, k, v (leaves) and dO, bf16 N(0, 1); q and k QK-normalised as the
+    model's attention inputs are, or raw N(0, 1) as the reference's harness
+    draws them (bench_attention.py:47-48) with qk_norm=False."""
     import torch
     gen = torch.Generator(device=dev).manual_seed(seed)
     q = torch.randn((B, H, T, D), device=dev, generator=gen)
     k = torch.randn((B, H, T, D), device=dev, generator=gen)
-    q = (q * torch.rsqrt((q * q).mean(-1, keepdim=True) + 1e-5)).bfloat16()
-    k = (k * torch.rsqrt((k * k).mean(-1, keepdim=True) + 1e-5)).bfloat16()
+    if qk_norm:
+        q = q * torch.rsqrt((q * q).mean(-1, keepdim=True) + 1e-5)
+        k = k * torch.rsqrt((k * k).mean(-1, keepdim=True) + 1e-5)
+    q, k = q.bfloat16(), k.bfloat16()
     v = torch.randn((B, H, T, D), device=dev, generator=gen).bfloat16()
     do = torch.randn((B, H, T, D), device=dev, generator=gen).bfloat16()
     return [x.requires_grad_(True) for x in (q, k, v)] + [do]
@@ -114,15 +119,22 @@ def time_steps(step, steps, warmup, probe=None, settle_s=SETTLE_S):
     return dt
 
 
-def bench_attention(B, H, T, D, steps, warmup, dev, kind="asinh"):
+def bench_attention(B, H, T, D, steps, warmup, dev, kind="asinh", kw=None, sink=False,
+                    qk_norm=True):
+    """One fwd+bwd step of flash_attention; `kw` replaces the default call
+    (the model's guarded n=16, c=8 asinh, or plain softmax), `sink` passes a
+    zero sink logit of shape (1, H, 1, 1) as the reference's harness does
+    (bench_attention.py:49)."""
     import torch
     from algebraic_amd.kernels import flash_attention
-    q, k, v, do = make_attention_inputs(B, H, T, D, 1, dev)
-    kw = (dict(kind="asinh", n=16, c=8.0, range_guard=True) if kind == "asinh"
-          else dict(kind="softmax"))
+    q, k, v, do = make_attention_inputs(B, H, T, D, 1, dev, qk_norm=qk_norm)
+    if kw is None:
+        kw = (dict(kind="asinh", n=16, c=8.0, range_guard=True) if kind == "asinh"
+              else dict(kind="softmax"))
+    s = torch.zeros((1, H, 1, 1), dtype=torch.float32, device=dev) if sink else None
 
     def step():
-        o = flash_attention(q, k, v, **kw)
+        o = flash_attention(q, k, v, s, **kw)
         torch.autograd.grad(o, (q, k, v), do)
 
     bwd_probe = Probe("attn_bwd", steps)
@@ -140,7 +152,8 @@ def bench_attention(B, H, T, D, steps, warmup, dev, kind="asinh"):
     }
 
 
-def bench_head(steps, warmup, dev, N=16384, d=768, V=50304, kind="alg_ce", n=8, c=2.0):
+def bench_head(steps, warmup, dev, N=16384, d=768, V=50304, kind="alg_ce", n=8, c=2.0,
+               library=True):
     import torch
     from algebraic_amd.kernels import fused_head
     gen = torch.Generator(device=dev).manual_seed(2)
@@ -164,7 +177,8 @@ def bench_head(steps, warmup, dev, N=16384, d=768, V=50304, kind="alg_ce", n=8, 
     return {"workload": f"N={N},d={d},V={V},{kind} n={n} c={c}", "ms_per_step": dt * 1e3,
             "tokens_per_s": N / dt, "tflops": flops / dt / 1e12,
             "frac": flops / dt / 1e12 / PEAK_BF16_TFLOPS, **split,
-            "library_gemm_tflops": library_gemm_rates(h.detach(), E.detach())}
+            **({"library_gemm_tflops": library_gemm_rates(h.detach(), E.detach())}
+               if library else {})}
 
 
 def library_gemm_rates(h, E, iters=10):
@@ -197,10 +211,50 @@ def library_gemm_rates(h, E, iters=10):
     return out
 
 
+def bench_harness_variants(steps, warmup, dev):
+    """The reference harness's attention sweep at configs[1]'s shape
+    (bench_attention.py:75-80): softmax with a zero sink, and asinh n=16,
+    c=16 shifted (exact rho), shifted + fast rho and unshifted + fast rho,
+    each with a zero sink, on raw N(0, 1) bf16 q, k, v as the harness draws
+    them; fwd+bwd step time and the forward and backward kernel times."""
+    B, H, T, D = 8, 12, 2048, 64
+    cases = {"softmax+sink": dict(kind="softmax")}
+    for shift, fast in ((True, False), (True, True), (False, True)):
+        name = f"asinh16/16 {'shift' if shift else 'noshift'}{'+fast' if fast else ''}"
+        cases[name] = dict(kind="asinh", n=16, c=16.0, shift=shift, fast_rho=fast)
+    out = {"workload": "bench_attention.py:75-80 at B=8,H=12,T=2048,D=64 bf16, raw N(0,1) "
+                       "q,k,v, zero sink (1,H,1,1)"}
+    for name, kw in cases.items():
+        a = bench_attention(B, H, T, D, steps, warmup, dev, kw=kw, sink=True, qk_norm=False)
+        out[name] = {"ms_per_step": round(a["ms_per_step"], 4), "tflops": round(a["tflops"], 2),
+                     "frac": round(a["tflops"] / PEAK_BF16_TFLOPS, 4),
+                     "fwd_kernel_ms": round(a["fwd_kernel_ms"], 4),
+                     "bwd_kernel_ms": round(a["bwd_kernel_ms"], 4)}
+    return out
+
+
+class CacheFlush:
+    """A 1 GiB buffer read between timed calls: it evicts the 256 MB Infinity
+    Cache (and the L2s), so the next call's operands come from HBM. It is
+    read, not written, so the cache holds clean lines afterwards and no
+    write-back of the flush itself overlaps the timed call."""
+
+    def __init__(self, dev):
+        import torch
+        self.buf = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+
+    def __call__(self):
+        self.buf.amax()
+
+
 def bench_qknorm(steps, warmup, dev):
     """QK-norm over the attention's q and k ([8, 2048, 16, 64] bf16 each) in
     one launch each way (qk_rms_norm_pair); the per-tensor calls are timed
-    beside it."""
+    beside it. Each is timed warm (the step repeated back to back: its
+    134 MB / 201 MB of operands largely stay in the 256 MB Infinity Cache)
+    and cold (a 1 GiB read between steps), next to a plain device copy of
+    the same bytes (torch copy_, one read and one write per element) as the
+    ceiling a streaming kernel of that size reaches in the same run."""
     import torch
     from algebraic_amd.kernels import qk_rms_norm, qk_rms_norm_pair
     gen = torch.Generator(device=dev).manual_seed(3)
@@ -230,12 +284,60 @@ def bench_qknorm(steps, warmup, dev):
     # separate 128-block launch); the per-tensor probe holds the k call.
     fwd_bytes, bwd_bytes = elems * 4, elems * 6
     f_ms, b_ms = fp.mean_ms(), bp.mean_ms()
-    return {"workload": "q,k each [8,2048,16,64] bf16, D=64 rows, one launch for both",
-            "fwd_us": f_ms * 1e3, "fwd_gbs": fwd_bytes / f_ms / 1e6,
-            "bwd_us": b_ms * 1e3, "bwd_gbs": bwd_bytes / b_ms / 1e6,
-            "fwd_frac": fwd_bytes / f_ms / 1e6 / PEAK_HBM_GBS,
-            "bwd_frac": bwd_bytes / b_ms / 1e6 / PEAK_HBM_GBS,
-            "per_tensor_fwd_us": sfp.mean_ms() * 1e3, "per_tensor_bwd_us": sbp.mean_ms() * 1e3}
+    out = {"workload": "q,k each [8,2048,16,64] bf16, D=64 rows, one launch for both",
+           "fwd_us": f_ms * 1e3, "fwd_gbs": fwd_bytes / f_ms / 1e6,
+           "bwd_us": b_ms * 1e3, "bwd_gbs": bwd_bytes / b_ms / 1e6,
+           "fwd_frac": fwd_bytes / f_ms / 1e6 / PEAK_HBM_GBS,
+           "bwd_frac": bwd_bytes / b_ms / 1e6 / PEAK_HBM_GBS,
+           "per_tensor_fwd_us": sfp.mean_ms() * 1e3, "per_tensor_bwd_us": sbp.mean_ms() * 1e3}
+    out["per_tensor_fwd_frac"] = fwd_bytes / 2 / sfp.mean_ms() / 1e6 / PEAK_HBM_GBS
+    out["per_tensor_bwd_frac"] = bwd_bytes / 2 / sbp.mean_ms() / 1e6 / PEAK_HBM_GBS
+
+    # Cold: the Infinity Cache flushed before every timed call.
+    flush = CacheFlush(dev)
+
+    def cold(step, probe, n):
+        for i in range(n):
+            flush()
+            probe.arm(i)
+            step()
+        probe.disarm()
+        torch.cuda.synchronize()
+
+    for name, step, nbytes in (("pair", pair_step, (fwd_bytes, bwd_bytes)),
+                               ("per_tensor", single_step, (fwd_bytes / 2, bwd_bytes / 2))):
+        cf, cb = Probe("qknorm_fwd", steps), Probe("qknorm_bwd", steps)
+        cold(step, cf, steps)
+        cold(step, cb, steps)
+        out[f"cold_{name}_fwd_us"] = cf.mean_ms() * 1e3
+        out[f"cold_{name}_fwd_frac"] = nbytes[0] / cf.mean_ms() / 1e6 / PEAK_HBM_GBS
+        out[f"cold_{name}_bwd_us"] = cb.mean_ms() * 1e3
+        out[f"cold_{name}_bwd_frac"] = nbytes[1] / cb.mean_ms() / 1e6 / PEAK_HBM_GBS
+
+    # Plain-copy ceilings at the per-tensor and pair sizes (67.1 / 134.2 MB
+    # moved), warm and cold, event-timed per call.
+    for name, n in (("per_tensor", xs[0].numel()), ("pair", 2 * xs[0].numel())):
+        src = torch.ones(n, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        for tag, pre in (("warm", None), ("cold", flush)):
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(steps)]
+            for _ in range(3):
+                dst.copy_(src)
+            for a, b in ev:
+                if pre is not None:
+                    pre()
+                a.record()
+                dst.copy_(src)
+                b.record()
+            torch.cuda.synchronize()
+            ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+            out[f"copy_{name}_{tag}_us"] = ms * 1e3
+            out[f"copy_{name}_{tag}_frac"] = 4 * n / ms / 1e6 / PEAK_HBM_GBS
+        del src, dst
+    del flush
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_elementwise(steps, warmup, dev):
@@ -407,6 +509,18 @@ def run_once(which, dev, steps=3):
         for _ in range(steps):
             o = flash_attention(q, k, v, kind="asinh", n=16, c=8.0, range_guard=True)
             torch.autograd.grad(o, (q, k, v), do)
+    elif which == "attn_harness":
+        # bench_attention.py:75-80's four variants at configs[1], zero sink
+        from algebraic_amd.kernels import flash_attention
+        q, k, v, do = make_attention_inputs(8, 12, 2048, 64, 1, dev, qk_norm=False)
+        sink = torch.zeros((1, 12, 1, 1), dtype=torch.float32, device=dev)
+        cases = [dict(kind="softmax")] + [
+            dict(kind="asinh", n=16, c=16.0, shift=sh, fast_rho=fa)
+            for sh, fa in ((True, False), (True, True), (False, True))]
+        for kw in cases:
+            for _ in range(steps):
+                o = flash_attention(q, k, v, sink, **kw)
+                torch.autograd.grad(o, (q, k, v), do)
     elif which == "head":
         from algebraic_amd.kernels import fused_head
         N, d, V = 16384, 768, 50304
@@ -596,10 +710,11 @@ def main():
                          "inputs, rocm-smi sampling)")
     ap.add_argument("--ns-only", action="store_true",
                     help="print only the Newton-Schulz line (Muon at the 350M model's shapes)")
-    ap.add_argument("--once", choices=("attn", "attn16", "head", "qknorm"),
+    ap.add_argument("--once", choices=("attn", "attn16", "attn_harness", "head", "qknorm"),
                     help="run three untimed steps of one workload and exit, printing nothing "
                          "else: the command for rocprofv3 counter passes (configs[1] attention, "
-                         "configs[3] attention, configs[2] head, configs[3] QK-norm)")
+                         "configs[3] attention, the reference harness's four attention "
+                         "variants, configs[2] head, configs[3] QK-norm)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 256 MiB device copy (scale reference for the "
                          "FETCH_SIZE/WRITE_SIZE counters of a rocprofv3 --pmc run)")
@@ -674,6 +789,12 @@ def main():
                      "traffic": bwd_counters().get("bytes_per_launch"),
                      "mfma_busy": bwd_counters().get("mfma_busy"),
                      "valu_busy": bwd_counters().get("valu_busy"),
+                     # traffic / mfma_busy / valu_busy are not measured by this
+                     # run: they are read from the committed counter summary
+                     "counters_from": ({"file": "profiles/attn_bwd_traffic.json",
+                                        "kernel": bwd_counters().get("kernel"),
+                                        "measured_in_this_run": False}
+                                       if bwd_counters() else None),
                      "flops_per_launch": a["bwd_flops"],
                      "avg_launch_ms": round(a["bwd_kernel_ms"], 4)},
         "step_frac_of_peak": round(a["tflops"] / PEAK_BF16_TFLOPS, 4),
@@ -687,6 +808,7 @@ def main():
     if not args.no_secondary:
         a16 = bench_attention(8, 16, T, D, max(5, args.steps // 2), 2, dev)
         asm = bench_attention(B, H, T, D, max(5, args.steps // 2), 2, dev, kind="softmax")
+        harness = bench_harness_variants(max(5, args.steps // 2), 2, dev)
         # The memory-bound lines run before the head, whose step and library
         # comparison allocate ~5 GB (the 1.65 GB dz among them).
         qk = bench_qknorm(20, 3, dev)
@@ -701,8 +823,18 @@ def main():
                              "ms_per_step": round(asm["ms_per_step"], 4),
                              "tflops": round(asm["tflops"], 2),
                              "frac": round(asm["tflops"] / PEAK_BF16_TFLOPS, 4)},
+            "attn_harness_variants": harness,
             "fused_head": {k: (round(v, 4) if isinstance(v, float) else v)
                            for k, v in bench_head(5, 2, dev).items()},
+            # bench_head.py:48-55: alg_ce at the harness's defaults (n=16,
+            # c=16), and the cross entropy, at configs[2]
+            "fused_head_alg_ce_n16_c16": {
+                k: (round(v, 4) if isinstance(v, float) else v)
+                for k, v in bench_head(5, 2, dev, kind="alg_ce", n=16, c=16.0,
+                                       library=False).items()},
+            "fused_head_ce": {k: (round(v, 4) if isinstance(v, float) else v)
+                              for k, v in bench_head(5, 2, dev, kind="ce", n=16, c=16.0,
+                                                     library=False).items()},
             "qknorm": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in qk.items()},
             "elementwise": {k: (round(v, 4) if isinstance(v, float) else v)
                             for k, v in ew.items()},

@@ -42,7 +42,9 @@ typedef struct {
   int32_t precise_output;  /* also write the float32 output (o_precise)        */
   float clamp;             /* score clamp when !shift && !bounded_scores       */
   int32_t poly_rho;        /* bounded radical (radical.py:26-38): polynomial   *
-                            * on |x| <= 1; asinh, shift=False, n = 16 only     */
+                            * on |x| <= 1; asinh, shift=False, n = 16 and     *
+                            * bounded_scores=0 only (the reference refuses    *
+                            * range_guard with it, flash.py:835-836)          */
 } algx_attn_variant;
 
 /* Text of the last error on this thread ("" when none). */
@@ -155,8 +157,8 @@ int32_t algx_attn_forward(const void* q, const void* k, const void* v, const flo
  * hipMalloc). Same arguments and results, no workspace: the guard's partial
  * maxima live in a static per-device scratch array of the library (768 KiB,
  * held by each GPU the library runs on until the process ends), so
- * B * H * T / 128 may not exceed 65536 on the MFMA shapes (a larger call
- * returns an error). Every call on one GPU shares that array: calls that
+ * B * H * T / 128 may not exceed 65536 whenever a guard word is given (a
+ * larger call returns an error before any other check or launch). Every call on one GPU shares that array: calls that
  * overlap on one GPU (concurrent streams) race. */
 int32_t algx_attn_forward_noalloc(const void* q, const void* k, const void* v, const float* sink,
                                   void* q_s, void* o, float* o_precise, float* stat,
@@ -202,7 +204,7 @@ int32_t algx_head_bwd(const void* h, const void* E, const int32_t* targets, cons
  *   y = cast((x * rsqrt(mean(x^2) + eps)) * gain)
  * gain: D float32, or NULL for the parameter-free AVN (model.py:142).
  * x, y, dy, dx: rows x D in dtype, D a multiple of 8 (bf16) or 4 (f32), at most
- * 1024. The backward is the autodiff VJP of that expression; dgain (D float32)
+ * 2048. The backward is the autodiff VJP of that expression; dgain (D float32)
  * is written exactly when gain is given, and then needs the workspace. */
 int32_t algx_rms_norm_fwd(const void* x, const float* gain, void* y, int64_t rows, int32_t D,
                           int32_t dtype, float eps, void* stream);

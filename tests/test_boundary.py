@@ -92,6 +92,42 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert rc != 0 and b"attn_prepare: q, k, v" in lib.algx_last_error()
 
 
+def test_attn_variant_rejects_polynomial_with_bounded_scores():
+    """The polynomial radical never pairs with the guard's unclamped low
+    variant (flash.py:835-836 refuses range_guard with poly_rho): the C ABI
+    refuses that variant before any launch."""
+    lib = _lib.load()
+    v = _lib.AttnVariant(kind=1, n=16, shift=0, fast_rho=1, inv_stat=1, bounded_scores=1,
+                         clamp=63.75, poly_rho=1)
+    rc = lib.algx_attn_fwd(None, None, None, None, None, None, None, 1, 1, 128, 64, 0,
+                           v, None, None, None)
+    assert rc != 0 and b"bounded_scores=0" in lib.algx_last_error()
+
+
+def test_noalloc_forward_rejects_sizes_beyond_its_scratch(monkeypatch):
+    """More than 65536 forward workgroups (B H T / 128) is refused by the
+    no-allocation forward before any other check or launch, on every path
+    (the generic-path switch set or not); no device pointer is passed."""
+    lib = _lib.load()
+    var = _lib.AttnVariant(kind=1, n=16, shift=0, fast_rho=1, inv_stat=1, bounded_scores=1,
+                           clamp=63.75)
+    guard = ctypes.c_void_p(512)   # never dereferenced: the size check comes first
+    for force in (None, "1"):
+        if force is None:
+            monkeypatch.delenv("ALGX_FORCE_GENERIC", raising=False)
+        else:
+            monkeypatch.setenv("ALGX_FORCE_GENERIC", force)
+        rc = lib.algx_attn_forward_noalloc(None, None, None, None, None, None, None, None, guard,
+                                           64, 32, 4352, 64, _lib.BF16, 0.125, 16.0, 1e8,
+                                           var, var, None)
+        assert rc != 0 and b"65536" in lib.algx_last_error()
+        # at the limit the size check passes and the null inputs are refused
+        rc = lib.algx_attn_forward_noalloc(None, None, None, None, None, None, None, None, guard,
+                                           64, 32, 4096, 64, _lib.BF16, 0.125, 16.0, 1e8,
+                                           var, var, None)
+        assert rc != 0 and b"null pointer" in lib.algx_last_error()
+
+
 def test_grouped_gemm_validation_without_a_gpu():
     """algx_gemm_bf16_grouped checks the group count and every group's
     arguments before it launches; empty groups launch nothing."""

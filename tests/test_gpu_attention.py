@@ -188,16 +188,21 @@ def test_whole_head_model_shape(mode):
         assert_bf16(a, b, what=f"{mode}:{nm}")
 
 
+@pytest.mark.parametrize("qscale", [1.0, 3.0])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("blocks", [(128, 128), (128, 256), (256, 128)])
-def test_model_attention_polynomial_radical(dtype, blocks):
+def test_model_attention_polynomial_radical(dtype, blocks, qscale):
     """test_flash_kernel_tpu.py:69-97, mode "polynomial": poly_rho (the
     bounded radical, radical.py:26-38) at n=16, c=8 with a sink against the
     exact functions with the reference's tolerances; and against the oracle's
     restatement of the reference's per-tile choice, within the polynomial's
-    approximation error (the kernels choose per score)."""
+    approximation error (the kernels choose per score). qscale 3 puts the
+    largest |x| near 2, so score tiles cross |x| = 1 and the per-score and
+    per-tile choices differ."""
     shape = (1, 2, 512, 64)
     q, k, v, g = _rand(shape, 13, dtype=dtype)
+    if qscale != 1.0:
+        q = (q.float() * qscale).to(q.dtype)
     sink = torch.from_numpy(np.random.default_rng(14).standard_normal((1, 2, 1, 1)).astype(np.float32))
     kw = dict(kind="asinh", n=16, c=8.0, shift=False, fast_rho=True, inv_stat=True)
     bq, bk = blocks

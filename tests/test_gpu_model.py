@@ -17,16 +17,21 @@ autograd of ``oracle.model`` on the same parameters and tokens.
   relative L2) which every operator meets in its own tests.
 
 Plus the 350M algebraic preset at its real width for one sequence of 2048
-tokens and V = 50304 (finite objective and gradients, the MFMA paths), and
+tokens and V = 50304 (finite objective and gradients, the MFMA paths); both
+350M presets at configs[4]'s full size (B = 8 x 2048) through a whole
+training step, with the final head checked against dense float32 math; and
 rematerialisation against no rematerialisation.
 """
+
+import math
 
 import numpy as np
 import pytest
 import torch
 
-from _tol import rel_l2
+from _tol import rel_l2, to_np
 from algebraic_amd import config, model
+from algebraic_amd.kernels import fused_head
 from oracle import model as OM
 
 pytestmark = pytest.mark.gpu
@@ -136,6 +141,107 @@ def test_350m_algebraic_step_is_finite():
     for name, t in _flat(params).items():
         assert t.grad is not None and torch.isfinite(t.grad).all(), name
     assert float(params["layers"]["w_q"].grad.abs().max()) > 0
+
+
+def _dense_head_slice(h, E, t, cfg, n_total):
+    """Dense float32 head on one slice of tokens (h (M, d) bf16, E (V, d)):
+    the objective's gradients w.r.t. h and E scaled as the slice's part of a
+    mean over n_total tokens. alg_ce differentiates the exact NLL of
+    log_softmax(n asinh(z/c)) (the reference's custom VJP,
+    algebraic.py:255-262), ce the cross entropy (standard.py:41-47)."""
+    rh = h.detach().float().requires_grad_(True)
+    re = E.detach().to(torch.bfloat16).float().requires_grad_(True)
+    z = rh @ re.T
+    logits = cfg.head_n * torch.asinh(z / cfg.head_c) if cfg.head == "alg_ce" else z
+    logp = torch.log_softmax(logits, -1).gather(1, t[:, None].long())[:, 0]
+    (-logp.sum() / n_total).backward()
+    return rh.grad, re.grad, logp.detach()
+
+
+@pytest.mark.parametrize("preset", ["algebraic", "standard"])
+def test_350m_training_step_at_benchmark_shape(preset):
+    """configs[4] at its stated size: the 350M preset (d 1024, 24 layers, 16
+    heads of 64, d_ff 2688, V 50304; model.py:196-231, config.py:17-42) on
+    B = 8 x T = 2048 random tokens, no rematerialisation, forward + backward
+    and one Muon + AdamW step (optimizers.py:118-246).
+
+    * the objective and the per-token telemetry against dense float32 math
+      on the model's final hidden states (mean(1 - p_t) just below one for
+      alg_ce at init; for ce the tied embedding puts each position's own
+      input token far ahead, so the cross entropy sits above ln V);
+    * every gradient finite and not all zero; every parameter finite and
+      changed by the step;
+    * the final head on the model's own last hidden states: the model's dh
+      for the first sequence (2048 tokens) against dense float32 math of that
+      slice's part of the mean, and the fused head called on that slice
+      alone (dh and dE) against the same dense math."""
+    from algebraic_amd import optimizers
+    B, T, V = 8, 2048, 50304
+    cfg = config.build(preset, "350m", vocab_size=V, seq_len=T, attn_impl="flash",
+                       head_impl="fused", remat=False)
+    params = model.init_params(cfg, seed=0, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    tok = torch.randint(0, V, (B, T + 1), generator=g, device=DEV)
+    x, y = tok[:, :-1].contiguous(), tok[:, 1:].contiguous()
+    tables = model.position_tables(cfg, T, device=DEV)
+    hidden = model.forward_hidden(params, x, cfg, tables)
+    hidden.retain_grad()
+    obj, tel = model.head_loss(params, hidden, y, cfg)
+    obj.backward()
+    torch.cuda.synchronize()
+    o = float(obj.detach())
+    assert math.isfinite(o) and torch.isfinite(tel).all()
+    # the objective and telemetry against dense float32 math over all B T
+    # tokens (2048 at a time)
+    E16 = params["embed"].detach().to(torch.bfloat16).float()
+    hs, ys = hidden.detach().reshape(B * T, -1), y.reshape(B * T)
+    lps = []
+    with torch.no_grad():
+        for i in range(0, B * T, T):
+            z = hs[i:i + T].float() @ E16.T
+            logits = cfg.head_n * torch.asinh(z / cfg.head_c) if cfg.head == "alg_ce" else z
+            lps.append(torch.log_softmax(logits, -1).gather(1, ys[i:i + T, None].long())[:, 0])
+    lp = torch.cat(lps)
+    del E16, lps
+    ref_obj = float((1.0 - lp.exp()).mean()) if cfg.head == "alg_ce" else float(-lp.mean())
+    assert abs(o - ref_obj) <= 2e-4 + 2e-3 * abs(ref_obj), (o, ref_obj)
+    want_tel = lp.exp() if cfg.head == "alg_ce" else -lp
+    np.testing.assert_allclose(to_np(tel), to_np(want_tel), rtol=2e-2, atol=2e-6)
+    if cfg.head == "alg_ce":
+        # mean(1 - p_t) with p_t far below one at init: just below one
+        assert 0.99 < o <= 1.0, o
+    flat = _flat(params)
+    for name, t in flat.items():
+        assert t.grad is not None and torch.isfinite(t.grad).all(), name
+        assert bool((t.grad != 0).any()), f"{name}: gradient is all zero"
+
+    # the head on the model's own final hidden states, first sequence
+    h0, t0 = hidden[0].detach(), y[0]
+    dh_ref, de_ref, logp = _dense_head_slice(h0, params["embed"], t0, cfg, B * T)
+    assert rel_l2(hidden.grad[0], dh_ref) <= 1e-2
+    th = h0.clone().requires_grad_(True)
+    te = params["embed"].detach().to(torch.bfloat16).requires_grad_(True)
+    s_obj, s_tel = fused_head(th, te, t0, kind=cfg.head, n=cfg.head_n, c=cfg.head_c)
+    s_obj.backward()
+    torch.cuda.synchronize()
+    want_tel = logp.exp() if cfg.head == "alg_ce" else -logp
+    np.testing.assert_allclose(to_np(s_tel), to_np(want_tel), rtol=2e-2, atol=2e-6)
+    # the slice alone averages over T tokens, the reference over B * T
+    assert rel_l2(th.grad.float() / B, dh_ref) <= 1e-2
+    assert rel_l2(te.grad.float() / B, de_ref) <= 1e-2
+    del dh_ref, de_ref, th, te
+
+    init_fn, step_fn = optimizers.get_optimizer("muon_adamw", 2e-3, weight_decay=0.1,
+                                                total_steps=100, warmup_fraction=0.0)
+    state = init_fn(params)
+    before = {k: v.detach().clone() for k, v in flat.items()}
+    step_fn(0, params, optimizers.grads_of(params), state, model.decay_mask(params))
+    torch.cuda.synchronize()
+    for name, t in _flat(params).items():
+        assert torch.isfinite(t).all(), name
+        assert not torch.equal(t.detach(), before[name]), f"{name}: unchanged by the step"
+    del params, before, state, hidden, flat
+    torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("preset", ["algebraic", "standard"])

@@ -71,15 +71,3 @@ def test_noalloc_forward_equals_workspace_forward(tail):
         assert got[0] == want[0] == (0 if tail else 1), (shape, got[0], want[0])
         for a, b, name in zip(got[1:], want[1:], ("q_s", "o", "stat", "o_precise")):
             assert torch.equal(a, b), (shape, name)
-
-
-def test_noalloc_forward_rejects_sizes_beyond_its_scratch():
-    """More than 65536 forward workgroups (B H T / 128) is refused before any
-    launch, with a message naming the limit."""
-    lib = _lib.load()
-    var = _c_variant(make_variant("asinh", 16, 8.0, seq_len=2048))
-    p = _lib.c_ptr(256)
-    guard = _lib.c_ptr(512)
-    rc = lib.algx_attn_forward_noalloc(p, p, p, None, p, p, p, p, guard, 64, 32, 4352, 64,
-                                       _lib.BF16, 0.125, 16.0, 1e8, var, var, None)
-    assert rc != 0 and b"65536" in lib.algx_last_error()
