@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libalgx.so"
 BF16, F32 = 0, 1
 SOFTMAX, ASINH = 0, 1
 HEAD_CE, HEAD_ALG_CE = 0, 1
+ATTN_WS_RAW, ATTN_WS_CLEARED = 0, 1
 GLU_ALU, GLU_SILU = 0, 1
 PROBE = {"none": 0, "attn_fwd": 1, "attn_bwd": 2, "head_fwd": 3, "head_dz": 4, "head_dh": 5,
          "head_de": 6, "qknorm_fwd": 7, "qknorm_bwd": 8, "rms_norm_fwd": 9, "rms_norm_bwd": 10,
@@ -57,13 +58,13 @@ SIGNATURES = {
     "algx_attn_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32,
                              _VP, _VP, _p, _p]),
     "algx_attn_forward_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
-    "algx_attn_forward": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32,
-                                 _i32, _f32, _f32, _f32, _VP, _VP, _p]),
-    "algx_attn_forward_noalloc": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32,
-                                         _i32, _i32, _f32, _f32, _f32, _VP, _VP, _p]),
+    "algx_attn_forward": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32,
+                                 _i32, _i32, _f32, _f32, _f32, _VP, _VP, _p]),
+    "algx_attn_forward_noalloc": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,
+                                         _i32, _i32, _i32, _f32, _f32, _f32, _VP, _VP, _p]),
     "algx_attn_bwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "algx_attn_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,
-                             _i32, _i32, _i32, _f32, _VP, _VP, _p, _p]),
+                             _i32, _i32, _i32, _i32, _f32, _VP, _VP, _p, _p]),
     "algx_head_fwd_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "algx_head_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _f32,
                              _i32, _p]),

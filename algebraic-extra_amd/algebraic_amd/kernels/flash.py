@@ -133,13 +133,20 @@ class _FlashFn(torch.autograd.Function):
         if guard is not None:
             ws = torch.empty(_lib.query("algx_attn_forward_workspace_bytes", B, H, T, D),
                              dtype=torch.uint8, device=dev)
+        # When a backward will follow, its workspace is allocated here and
+        # prepared by the forward in passing (its dQ accumulator cleared).
+        bws = None
+        if any(ctx.needs_input_grad[:4]):
+            bws = torch.empty(_lib.query("algx_attn_bwd_workspace_bytes", B, H, T, D),
+                              dtype=torch.uint8, device=dev)
         lo = _c_variant(plan.low)
         hi = _c_variant(plan.high) if plan.high is not None else None
         _lib.call("algx_attn_forward", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
                   _lib.ptr(q_s), _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat),
-                  _lib.ptr(guard), _lib.ptr(ws), B, H, T, D, dt, plan.q_scale, plan.bound,
-                  plan.vmax, lo, hi, st)
+                  _lib.ptr(guard), _lib.ptr(ws), _lib.ptr(bws), B, H, T, D, dt, plan.q_scale,
+                  plan.bound, plan.vmax, lo, hi, st)
         ctx.plan = plan
+        ctx.bws = bws
         ctx.save_for_backward(q_s, k, v, sink, o, o_precise, stat, guard)
         return o
 
@@ -152,13 +159,19 @@ class _FlashFn(torch.autograd.Function):
         do = do.to(q_s.dtype).contiguous()
         dq, dk, dv = torch.empty_like(q_s), torch.empty_like(k), torch.empty_like(v)
         dsink = torch.empty((H,), dtype=torch.float32, device=q_s.device) if sink is not None else None
-        ws = torch.empty(_lib.query("algx_attn_bwd_workspace_bytes", B, H, T, D),
-                         dtype=torch.uint8, device=q_s.device)
+        # The forward's prepared workspace serves one backward; a second one
+        # (retain_graph) hands it over as raw memory.
+        ws, state = ctx.bws, _lib.ATTN_WS_CLEARED
+        ctx.bws = None
+        if ws is None:
+            ws = torch.empty(_lib.query("algx_attn_bwd_workspace_bytes", B, H, T, D),
+                             dtype=torch.uint8, device=q_s.device)
+            state = _lib.ATTN_WS_RAW
         lo = _c_variant(plan.low)
         hi = _c_variant(plan.high) if plan.high is not None else None
         _lib.call("algx_attn_bwd", _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
                   _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat), _lib.ptr(do),
-                  _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dsink), _lib.ptr(ws),
+                  _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dsink), _lib.ptr(ws), state,
                   B, H, T, D, dt, plan.q_scale, lo, hi, _lib.ptr(guard), _lib.stream())
         return dq, dk, dv, dsink, None
 

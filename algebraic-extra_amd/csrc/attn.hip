@@ -152,10 +152,10 @@ extern "C" int64_t algx_attn_forward_workspace_bytes(int32_t B, int32_t H, int32
 
 extern "C" int32_t algx_attn_forward(const void* q, const void* k, const void* v,
                                      const float* sink, void* q_s, void* o, float* o_precise,
-                                     float* stat, int32_t* guard, void* workspace, int32_t B,
-                                     int32_t H, int32_t T, int32_t D, int32_t dtype,
-                                     float q_scale, float bound, float vmax,
-                                     const algx_attn_variant* low,
+                                     float* stat, int32_t* guard, void* workspace,
+                                     void* bwd_workspace, int32_t B, int32_t H, int32_t T,
+                                     int32_t D, int32_t dtype, float q_scale, float bound,
+                                     float vmax, const algx_attn_variant* low,
                                      const algx_attn_variant* high, void* stream) {
   if (int32_t rc = check_shape(B, H, T, D, dtype)) return rc;
   KVariant kl{}, kh{};
@@ -171,13 +171,15 @@ extern "C" int32_t algx_attn_forward(const void* q, const void* k, const void* v
     return fail("attn_forward: null pointer");
   if ((kl.precise || (guard != nullptr && kh.precise)) && o_precise == nullptr)
     return fail("attn_forward: precise-output variant needs o_precise");
-  if (int32_t rc = check_aligned("attn_forward", {q, k, v, q_s, o, o_precise})) return rc;
+  if (int32_t rc = check_aligned("attn_forward", {q, k, v, q_s, o, o_precise, bwd_workspace}))
+    return rc;
   hipStream_t s = (hipStream_t)stream;
   if (mfma_supported(T, D, dtype) && !force_generic()) {
     if (guard != nullptr && workspace == nullptr)
       return fail("attn_forward: the guard needs the workspace");
-    return launch_fwd_fused(q, k, v, sink, q_s, o, o_precise, stat, guard, (float*)workspace, B,
-                            H, T, q_scale, bound, vmax, kl, kh, s);
+    // The backward workspace starts with its float32 dQ accumulator.
+    return launch_fwd_fused(q, k, v, sink, q_s, o, o_precise, stat, guard, (float*)workspace,
+                            (float*)bwd_workspace, B, H, T, q_scale, bound, vmax, kl, kh, s);
   }
   if (int32_t rc = launch_prepare(q, k, v, sink, q_s, guard, B, H, T, D, dtype, q_scale, bound,
                                   vmax, s))
@@ -201,10 +203,10 @@ extern "C" int64_t algx_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t T
 extern "C" int32_t algx_attn_bwd(const void* q, const void* k, const void* v, const float* sink,
                                  const void* o, const float* o_precise, const float* stat,
                                  const void* dout, void* dq, void* dk, void* dv, float* dsink,
-                                 void* workspace, int32_t B, int32_t H, int32_t T, int32_t D,
-                                 int32_t dtype, float q_scale, const algx_attn_variant* low,
-                                 const algx_attn_variant* high, const int32_t* guard,
-                                 void* stream) {
+                                 void* workspace, int32_t workspace_state, int32_t B, int32_t H,
+                                 int32_t T, int32_t D, int32_t dtype, float q_scale,
+                                 const algx_attn_variant* low, const algx_attn_variant* high,
+                                 const int32_t* guard, void* stream) {
   if (int32_t rc = check_shape(B, H, T, D, dtype)) return rc;
   KVariant kl{}, kh{};
   if (int32_t rc = to_kvar(low, kl, "low")) return rc;
@@ -213,6 +215,8 @@ extern "C" int32_t algx_attn_bwd(const void* q, const void* k, const void* v, co
   } else {
     kh = kl;
   }
+  if (workspace_state != ALGX_ATTN_WS_RAW && workspace_state != ALGX_ATTN_WS_CLEARED)
+    return fail("attn_bwd: workspace_state must be ALGX_ATTN_WS_RAW or ALGX_ATTN_WS_CLEARED");
   hipStream_t s = (hipStream_t)stream;
   const int64_t rows = (int64_t)B * H * T;
   if (rows == 0) {
@@ -229,8 +233,12 @@ extern "C" int32_t algx_attn_bwd(const void* q, const void* k, const void* v, co
   const bool mfma = mfma_supported(T, D, dtype) && !force_generic();
   float* dq_acc = (float*)workspace;
   float* di = (float*)((char*)workspace + rows * D * (int64_t)sizeof(float));
-  if (int32_t rc = launch_bwd_pre(dout, o, o_precise, stat, sink, di, mfma ? dq_acc : nullptr,
-                                  dsink, B, H, T, D, dtype, kl, kh, guard, s))
+  // The pre-pass forms di and dsink, and clears the dQ accumulator unless
+  // the forward already did (a workspace it prepared).
+  const bool cleared = mfma && workspace_state == ALGX_ATTN_WS_CLEARED;
+  if (int32_t rc = launch_bwd_pre(dout, o, o_precise, stat, sink, di,
+                                  mfma && !cleared ? dq_acc : nullptr, dsink, B, H, T, D, dtype,
+                                  kl, kh, guard, s))
     return rc;
   if (mfma) {
     if (int32_t rc = launch_bwd_mfma(q, k, v, stat, di, dout, dq_acc, dk, dv, B, H, T, kl, kh,
@@ -252,7 +260,8 @@ extern "C" int32_t algx_attn_bwd(const void* q, const void* k, const void* v, co
 extern "C" int32_t algx_attn_forward_noalloc(const void* q, const void* k, const void* v,
                                              const float* sink, void* q_s, void* o,
                                              float* o_precise, float* stat, int32_t* guard,
-                                             int32_t B, int32_t H, int32_t T, int32_t D,
+                                             void* bwd_workspace, int32_t B, int32_t H,
+                                             int32_t T, int32_t D,
                                              int32_t dtype, float q_scale, float bound,
                                              float vmax, const algx_attn_variant* low,
                                              const algx_attn_variant* high, void* stream) {
@@ -270,6 +279,6 @@ extern "C" int32_t algx_attn_forward_noalloc(const void* q, const void* k, const
       !force_generic()) {
     if (int32_t rc = scratch_on_current_device(&part)) return rc;
   }
-  return algx_attn_forward(q, k, v, sink, q_s, o, o_precise, stat, guard, part, B, H, T, D,
-                           dtype, q_scale, bound, vmax, low, high, stream);
+  return algx_attn_forward(q, k, v, sink, q_s, o, o_precise, stat, guard, part, bwd_workspace, B,
+                           H, T, D, dtype, q_scale, bound, vmax, low, high, stream);
 }

@@ -13,6 +13,8 @@ int32_t launch_prepare(const void* q, const void* k, const void* v, const float*
 // Guard word from `nblocks` triples of partial maxima (|q_s|^2, |k|^2, |v|).
 int32_t launch_guard_finish(const float* partial, int nblocks, const float* sink, int H,
                             float bound, float vmax, int32_t* guard, hipStream_t s);
+// Row pre-pass of the backward: di (and the sink gradient), and the dQ
+// accumulator cleared when dq_acc is given.
 int32_t launch_bwd_pre(const void* dout, const void* o, const float* o_precise,
                        const float* stat, const float* sink, float* di, float* dq_acc,
                        float* dsink, int B, int H, int T, int D, int dtype, const KVariant& low,
@@ -44,12 +46,14 @@ int32_t launch_fwd_mfma(const void* q_s, const void* k, const void* v, const flo
 // variant runs over the whole grid writing q_s and, guarded, one triple of
 // partial maxima per workgroup (fwd_fused_partials of them); a second launch
 // reduces them to the guard word and, out of range only, runs the high
-// variant.
+// variant. dq_zero (or null): the backward's dQ accumulator, cleared in the
+// same pass.
 int64_t fwd_fused_partials(int B, int H, int T);
 int32_t launch_fwd_fused(const void* q, const void* k, const void* v, const float* sink,
                          void* q_s, void* o, float* o_precise, float* stat, int32_t* guard,
-                         float* partial, int B, int H, int T, float q_scale, float bound,
-                         float vmax, const KVariant& lo, const KVariant& hi, hipStream_t s);
+                         float* partial, float* dq_zero, int B, int H, int T, float q_scale,
+                         float bound, float vmax, const KVariant& lo, const KVariant& hi,
+                         hipStream_t s);
 int32_t launch_bwd_mfma(const void* q_s, const void* k, const void* v, const float* stat,
                         const float* di, const void* dout, float* dq_acc, void* dk, void* dv,
                         int B, int H, int T, const KVariant& lo, const KVariant& hi,

@@ -350,6 +350,13 @@ __device__ __forceinline__ void fwd_body(
     for (int ks = 0; ks < 4; ++ks) *reinterpret_cast<bf16x8*>(qsp + 16 * ks) = qreg[ks];
     if (prep.partial != nullptr && tid < 3) prep.partial[(int64_t)bid * 3 + tid] = part_out;
   }
+  if (prep.dq_zero != nullptr) {
+    // The workgroup's 128 query rows of the accumulator are one contiguous
+    // 32 KB run: eight coalesced 16-byte stores per thread.
+    f32x4* z = reinterpret_cast<f32x4*>(prep.dq_zero + base + (int64_t)q0 * HD);
+#pragma unroll
+    for (int i = 0; i < FBM * HD / 4 / 256; ++i) z[tid + 256 * i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
 }
 
 // The guard word (if any) picks the low or the high variant for the whole
@@ -477,8 +484,9 @@ int64_t fwd_fused_partials(int B, int H, int T) {
 
 int32_t launch_fwd_fused(const void* q, const void* k, const void* v, const float* sink,
                          void* q_s, void* o, float* o_precise, float* stat, int32_t* guard,
-                         float* partial, int B, int H, int T, float q_scale, float bound,
-                         float vmax, const KVariant& lo, const KVariant& hi, hipStream_t s) {
+                         float* partial, float* dq_zero, int B, int H, int T, float q_scale,
+                         float bound, float vmax, const KVariant& lo, const KVariant& hi,
+                         hipStream_t s) {
   using namespace mfma;
   const int grid = B * H * (T / FBM);
   // Low variant over the whole grid, fused with the pre-scale and (guarded)
@@ -486,7 +494,7 @@ int32_t launch_fwd_fused(const void* q, const void* k, const void* v, const floa
   // overwritten by the high launch below.
   FwdFn fn = pick_fwd(cfg_for(lo), cfg_for(lo));
   if (fn == nullptr) return fail("attn_forward: no MFMA kernel for the low variant");
-  FwdPrep pre{(bf16*)q_s, q_scale, guard != nullptr ? partial : nullptr};
+  FwdPrep pre{(bf16*)q_s, q_scale, guard != nullptr ? partial : nullptr, dq_zero};
   launch_k(probe_for(ALGX_PROBE_ATTN_FWD), fn, dim3(grid), dim3(256), s, (const bf16*)q,
            (const bf16*)k, (const bf16*)v, sink, (bf16*)o, o_precise, stat, H, T, lo, lo,
            (const int32_t*)nullptr, pre);

@@ -48,6 +48,9 @@ struct FwdPrep {
   bf16* q_s = nullptr;
   float q_scale = 1.0f;
   float* partial = nullptr;
+  // Non-null: the backward's float32 dQ accumulator ((B, H, T, 64)), whose
+  // rows of the workgroup's query block are set to zero in passing.
+  float* dq_zero = nullptr;
 };
 
 // s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt left unconstrained

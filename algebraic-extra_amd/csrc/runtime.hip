@@ -95,4 +95,4 @@ extern "C" int32_t algx_set_probe(int32_t which, void* start_event, void* stop_e
 
 extern "C" const char* algx_last_error(void) { return algx::g_error.c_str(); }
 
-extern "C" int32_t algx_version(void) { return 2; }
+extern "C" int32_t algx_version(void) { return 3; }

@@ -27,6 +27,11 @@ extern "C" {
 enum { ALGX_BF16 = 0, ALGX_F32 = 1 };
 enum { ALGX_SOFTMAX = 0, ALGX_ASINH = 1 };
 enum { ALGX_HEAD_CE = 0, ALGX_HEAD_ALG_CE = 1 };
+/* State of the backward workspace handed to algx_attn_bwd: RAW = contents
+ * unspecified; CLEARED = the same buffer was passed as bwd_workspace to the
+ * algx_attn_forward call whose outputs the backward receives, with no other
+ * use in between (its dQ accumulator is then already zero). */
+enum { ALGX_ATTN_WS_RAW = 0, ALGX_ATTN_WS_CLEARED = 1 };
 
 /* Numeric variant of the attention kernels; mirrors the numeric fields of the
  * reference's Variant (src/algebraic/kernels/flash.py:59-73). Schedule flags
@@ -143,12 +148,15 @@ int32_t algx_attn_fwd(const void* q_s, const void* k, const void* v, const float
  * (algx_attn_forward_workspace_bytes; may be NULL when guard is NULL). A
  * second launch reduces them to the guard word and, only when out of range,
  * recomputes the forward with `high`, completing lax.cond. Other shapes run
- * the two calls. */
+ * the two calls. bwd_workspace: NULL, or the algx_attn_bwd_workspace_bytes
+ * buffer the backward of this call will receive; the forward prepares it in
+ * passing so that algx_attn_bwd can take it as ALGX_ATTN_WS_CLEARED (the
+ * reference's forward has no such output: it spares the backward a pass). */
 int64_t algx_attn_forward_workspace_bytes(int32_t B, int32_t H, int32_t T, int32_t D);
 int32_t algx_attn_forward(const void* q, const void* k, const void* v, const float* sink,
                           void* q_s, void* o, float* o_precise, float* stat, int32_t* guard,
-                          void* workspace, int32_t B, int32_t H, int32_t T, int32_t D,
-                          int32_t dtype, float q_scale, float bound, float vmax,
+                          void* workspace, void* bwd_workspace, int32_t B, int32_t H, int32_t T,
+                          int32_t D, int32_t dtype, float q_scale, float bound, float vmax,
                           const algx_attn_variant* low, const algx_attn_variant* high,
                           void* stream);
 
@@ -162,7 +170,8 @@ int32_t algx_attn_forward(const void* q, const void* k, const void* v, const flo
  * overlap on one GPU (concurrent streams) race. */
 int32_t algx_attn_forward_noalloc(const void* q, const void* k, const void* v, const float* sink,
                                   void* q_s, void* o, float* o_precise, float* stat,
-                                  int32_t* guard, int32_t B, int32_t H, int32_t T, int32_t D,
+                                  int32_t* guard, void* bwd_workspace, int32_t B, int32_t H,
+                                  int32_t T, int32_t D,
                                   int32_t dtype, float q_scale, float bound, float vmax,
                                   const algx_attn_variant* low, const algx_attn_variant* high,
                                   void* stream);
@@ -170,13 +179,16 @@ int32_t algx_attn_forward_noalloc(const void* q, const void* k, const void* v, c
 int64_t algx_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t T, int32_t D);
 /* dq is w.r.t. the unscaled q: dq = cast(cast(dq_s) * q_scale) as autodiff of
  * flash.py:833 gives; dsink (H,) float32 is w.r.t. the kernel-unit sink
- * (flash.py:721-723) and may be NULL when sink is NULL. */
+ * (flash.py:721-723) and may be NULL when sink is NULL. workspace_state:
+ * ALGX_ATTN_WS_RAW, or ALGX_ATTN_WS_CLEARED for a workspace the forward
+ * prepared (see algx_attn_forward), whose dQ accumulator the backward then
+ * does not clear again. */
 int32_t algx_attn_bwd(const void* q_s, const void* k, const void* v, const float* sink,
                       const void* o, const float* o_precise, const float* stat, const void* dout,
-                      void* dq, void* dk, void* dv, float* dsink, void* workspace, int32_t B,
-                      int32_t H, int32_t T, int32_t D, int32_t dtype, float q_scale,
-                      const algx_attn_variant* low, const algx_attn_variant* high,
-                      const int32_t* guard, void* stream);
+                      void* dq, void* dk, void* dv, float* dsink, void* workspace,
+                      int32_t workspace_state, int32_t B, int32_t H, int32_t T, int32_t D,
+                      int32_t dtype, float q_scale, const algx_attn_variant* low,
+                      const algx_attn_variant* high, const int32_t* guard, void* stream);
 
 /* ------------------------------------------------------------ fused head
  * Replaces fused_head (src/algebraic/kernels/fused_head.py:260-275): forward

@@ -36,7 +36,7 @@ def test_library_loads_and_exports_every_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.algx_version() == 2
+    assert lib.algx_version() == 3
     assert lib.algx_last_error() == b""
 
 
@@ -82,12 +82,18 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     rc = lib.algx_attn_fwd(a, a, a, None, bad, None, a, 1, 1, 128, 64, 0, v, None, None, None)
     assert rc != 0 and b"attn_fwd" in lib.algx_last_error()
     assert b"16-byte aligned" in lib.algx_last_error()
-    rc = lib.algx_attn_forward(a, a, a, None, a, bad, None, a, None, None, 1, 1, 128, 64, 0,
-                               1.0, 1.0, 1.0, v, None, None)
+    rc = lib.algx_attn_forward(a, a, a, None, a, bad, None, a, None, None, None, 1, 1, 128, 64,
+                               0, 1.0, 1.0, 1.0, v, None, None)
     assert rc != 0 and b"attn_forward: q, k, v" in lib.algx_last_error()
-    rc = lib.algx_attn_bwd(a, a, a, None, a, None, a, a, bad, a, a, None, a, 1, 1, 128, 64, 0,
-                           1.0, v, None, None, None)
+    rc = lib.algx_attn_forward(a, a, a, None, a, a, None, a, None, None, bad, 1, 1, 128, 64,
+                               0, 1.0, 1.0, 1.0, v, None, None)
+    assert rc != 0 and b"attn_forward: q, k, v" in lib.algx_last_error()
+    rc = lib.algx_attn_bwd(a, a, a, None, a, None, a, a, bad, a, a, None, a, _lib.ATTN_WS_RAW,
+                           1, 1, 128, 64, 0, 1.0, v, None, None, None)
     assert rc != 0 and b"attn_bwd: q, k, v" in lib.algx_last_error()
+    rc = lib.algx_attn_bwd(a, a, a, None, a, None, a, a, a, a, a, None, a, 7, 1, 1, 128, 64, 0,
+                           1.0, v, None, None, None)
+    assert rc != 0 and b"workspace_state" in lib.algx_last_error()
     rc = lib.algx_attn_prepare(a, a, a, None, bad, None, 1, 1, 128, 64, 0, 1.0, 1.0, 1.0, None)
     assert rc != 0 and b"attn_prepare: q, k, v" in lib.algx_last_error()
 
@@ -118,12 +124,12 @@ def test_noalloc_forward_rejects_sizes_beyond_its_scratch(monkeypatch):
         else:
             monkeypatch.setenv("ALGX_FORCE_GENERIC", force)
         rc = lib.algx_attn_forward_noalloc(None, None, None, None, None, None, None, None, guard,
-                                           64, 32, 4352, 64, _lib.BF16, 0.125, 16.0, 1e8,
+                                           None, 64, 32, 4352, 64, _lib.BF16, 0.125, 16.0, 1e8,
                                            var, var, None)
         assert rc != 0 and b"65536" in lib.algx_last_error()
         # at the limit the size check passes and the null inputs are refused
         rc = lib.algx_attn_forward_noalloc(None, None, None, None, None, None, None, None, guard,
-                                           64, 32, 4096, 64, _lib.BF16, 0.125, 16.0, 1e8,
+                                           None, 64, 32, 4096, 64, _lib.BF16, 0.125, 16.0, 1e8,
                                            var, var, None)
         assert rc != 0 and b"null pointer" in lib.algx_last_error()
 

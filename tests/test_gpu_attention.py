@@ -314,8 +314,8 @@ def test_fused_forward_equals_prepare_then_forward(tail):
                              dtype=torch.uint8, device=DEV)
             _lib.call("algx_attn_forward", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
                       _lib.ptr(q_s), _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat),
-                      _lib.ptr(guard), _lib.ptr(ws), B, H, T, D, _lib.dtype_code(q.dtype),
-                      q_scale, bound, vmax, lo, hi, st)
+                      _lib.ptr(guard), _lib.ptr(ws), None, B, H, T, D,
+                      _lib.dtype_code(q.dtype), q_scale, bound, vmax, lo, hi, st)
         else:
             _lib.call("algx_attn_prepare", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink),
                       _lib.ptr(q_s), _lib.ptr(guard), B, H, T, D, _lib.dtype_code(q.dtype),
@@ -499,7 +499,8 @@ def test_precise_output_in_every_mode(kind, shift):
                          dtype=torch.uint8, device=DEV)
         _lib.call("algx_attn_bwd", _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), None, _lib.ptr(o),
                   _lib.ptr(o_precise), _lib.ptr(stat), _lib.ptr(do), _lib.ptr(dq), _lib.ptr(dk),
-                  _lib.ptr(dv), None, _lib.ptr(ws), B, H, T, D, _lib.BF16, 1.0, lo, None, None, st)
+                  _lib.ptr(dv), None, _lib.ptr(ws), _lib.ATTN_WS_RAW, B, H, T, D, _lib.BF16, 1.0,
+                  lo, None, None, st)
         torch.cuda.synchronize()
         if precise:
             assert torch.isfinite(o_precise).all()
@@ -508,3 +509,29 @@ def test_precise_output_in_every_mode(kind, shift):
     for a, b in zip(*outs):
         assert torch.isfinite(a.float()).all()
         assert rel_l2(a, b) <= 5e-3
+
+
+@pytest.mark.parametrize("kind", ["asinh", "softmax"])
+def test_prepared_workspace_backward_matches_raw(kind):
+    """flash_attention's backward runs on the workspace its forward prepared
+    (ALGX_ATTN_WS_CLEARED: the forward cleared the dQ accumulator, the
+    backward's pre-pass only forms di). A second backward of the same graph
+    (retain_graph) gets a raw workspace, which the pre-pass clears. Both
+    match the oracle; dk and dv agree bit for bit (dq sums float32 atomics in
+    an order that may vary from run to run)."""
+    B, H, T, D = 2, 3, 512, 64
+    q, k, v, g = _rand((B, H, T, D), 97)
+    kw = (dict(kind="asinh", n=16, c=8.0, range_guard=True) if kind == "asinh"
+          else dict(kind="softmax"))
+    tq, tk, tv = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
+    o = flash_attention(tq, tk, tv, None, **kw)
+    gd = g.to(DEV)
+    first = torch.autograd.grad(o, (tq, tk, tv), gd, retain_graph=True)
+    second = torch.autograd.grad(o, (tq, tk, tv), gd)
+    torch.cuda.synchronize()
+    (_, *want), _ = _oracle(q, k, v, g, None, "bf16", **kw)
+    for got in (first, second):
+        for a, b, nm in zip(got, want, ("dq", "dk", "dv")):
+            assert_bf16(to_np(a), b, what=nm)
+    assert torch.equal(first[1], second[1]) and torch.equal(first[2], second[2])
+    assert rel_l2(first[0], second[0]) <= 1e-3

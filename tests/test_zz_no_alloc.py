@@ -47,17 +47,21 @@ def _forward(q, k, v, sink, noalloc):
     q_s, o = torch.empty_like(q), torch.empty_like(q)
     stat = torch.empty((B, H, T), dtype=torch.float32, device=DEV)
     o_precise = torch.zeros(q.shape, dtype=torch.float32, device=DEV)
+    # The backward workspace the forward prepares: its dQ accumulator (the
+    # first B*H*T*D floats) starts as NaN and must come back zero.
+    bws = torch.full((_lib.query("algx_attn_bwd_workspace_bytes", B, H, T, D) // 4,),
+                     float("nan"), dtype=torch.float32, device=DEV)
     common = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink), _lib.ptr(q_s), _lib.ptr(o),
               _lib.ptr(o_precise), _lib.ptr(stat), _lib.ptr(guard))
     tail = (B, H, T, D, _lib.BF16, q_scale, bound, vmax, lo, hi, _lib.stream())
     if noalloc:
-        _lib.call("algx_attn_forward_noalloc", *common, *tail)
+        _lib.call("algx_attn_forward_noalloc", *common, _lib.ptr(bws), *tail)
     else:
         ws = torch.empty(_lib.query("algx_attn_forward_workspace_bytes", B, H, T, D),
                          dtype=torch.uint8, device=DEV)
-        _lib.call("algx_attn_forward", *common, _lib.ptr(ws), *tail)
+        _lib.call("algx_attn_forward", *common, _lib.ptr(ws), _lib.ptr(bws), *tail)
     torch.cuda.synchronize()
-    return int(guard[0].item()), q_s, o, stat, o_precise
+    return int(guard[0].item()), q_s, o, stat, o_precise, bws[: B * H * T * D]
 
 
 @pytest.mark.parametrize("tail", [False, True])
@@ -69,5 +73,6 @@ def test_noalloc_forward_equals_workspace_forward(tail):
         want = _forward(q, k, v, sink, noalloc=False)
         got = _forward(q, k, v, sink, noalloc=True)
         assert got[0] == want[0] == (0 if tail else 1), (shape, got[0], want[0])
-        for a, b, name in zip(got[1:], want[1:], ("q_s", "o", "stat", "o_precise")):
+        for a, b, name in zip(got[1:], want[1:], ("q_s", "o", "stat", "o_precise", "dq_acc")):
             assert torch.equal(a, b), (shape, name)
+        assert not got[5].any(), shape
