@@ -410,13 +410,18 @@ typedef void (*HeadDzFn)(const bf16*, const bf16*, const int32_t*, const float*,
                          bf16*, int64_t, int64_t, int, int, int, int, int, float, float, int);
 
 // Kernel instance for (kind, n): alg_ce with n = 8, 16 or 32 gets unrolled
-// powers. DMA (the direct-to-LDS ring) when d is a multiple of BK.
+// powers in both kernels, and the forward also for n = 2, 4 and 64 (its
+// runtime power loop, kept for n >= 128, spills registers). DMA (the
+// direct-to-LDS ring) when d is a multiple of BK.
 template <bool DMA> HeadFwdFn pick_head_fwd_as(int kind, int log2n) {
   if (kind == ALGX_HEAD_CE) return head_fwd_kernel<ALGX_HEAD_CE, 0, DMA>;
   switch (log2n) {
+    case 1: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 1, DMA>;
+    case 2: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 2, DMA>;
     case 3: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 3, DMA>;
     case 4: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 4, DMA>;
     case 5: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 5, DMA>;
+    case 6: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 6, DMA>;
     default: return head_fwd_kernel<ALGX_HEAD_ALG_CE, 0, DMA>;
   }
 }

@@ -125,6 +125,21 @@ def test_fused_head_matches_oracle(kind, n, c, V):
         assert cos > 0.999
 
 
+@pytest.mark.parametrize("n", [2, 4, 32, 64, 128])
+def test_fused_head_alg_ce_every_unrolled_power(n):
+    """alg_ce with the other powers of two: n = 2, 4, 32, 64 run forward
+    kernels with compile-time powers, n = 128 the runtime power loop; each
+    against the oracle (c = 4, clamp 0.25 (1e38 / V)^(1/n), fused_head.py:273)."""
+    h, e, t = _head_inputs(512, 128, 3000, 3, 0.15)
+    got = _head_run(h, e, t, kind="alg_ce", n=n, c=4.0)
+    (obj, tel), (dh, de) = OH.fused_head(to_np(h), to_np(e), to_np(t), kind="alg_ce", n=n,
+                                         c=4.0, dtype="bf16", g_obj=1.0)
+    assert abs(got[0] - obj) <= 2e-4 + 2e-3 * abs(obj)
+    np.testing.assert_allclose(got[1], tel, rtol=2e-2, atol=2e-4)
+    assert_bf16(got[2], dh, what=f"dh n={n}")
+    assert rel_l2(got[3], de) <= 1e-2
+
+
 @pytest.mark.parametrize("N,d,V", [(300, 64, 1000), (600, 40, 257), (8, 128, 300),
                                    (2048, 128, 16284)])
 def test_fused_head_ragged_tiles(N, d, V):
@@ -213,6 +228,8 @@ def test_fused_head_backward_over_token_chunks(monkeypatch):
     assert abs(float(obj) - ref) <= 2e-4 + 2e-3 * abs(ref)
     assert rel_l2(th.grad, rh.grad) <= 1e-2
     assert rel_l2(te.grad, re.grad) <= 1e-2
+    for a, b in ((th.grad, rh.grad), (te.grad, re.grad)):
+        assert float((a.float() - b).abs().max()) <= 2e-2 * float(b.abs().max())
 
 
 @pytest.mark.parametrize("kind,n,c", [("alg_ce", 8, 2.0), ("ce", 16, 16.0)])
@@ -244,3 +261,7 @@ def test_fused_head_at_benchmark_shape(kind, n, c):
     np.testing.assert_allclose(to_np(tel), to_np(want_tel.detach()), rtol=2e-2, atol=2e-6)
     assert rel_l2(th.grad, rh.grad) <= 1e-2
     assert rel_l2(te.grad, re.grad) <= 1e-2
+    # Elementwise: the gradients are O(1/N), so the bf16 bar's 2e-2 is taken
+    # relative to each tensor's largest entry (max |a - b| <= 2e-2 max |b|).
+    for a, b in ((th.grad, rh.grad), (te.grad, re.grad)):
+        assert float((a.float() - b).abs().max()) <= 2e-2 * float(b.abs().max())
