@@ -29,8 +29,8 @@ def pytest_collection_modifyitems(config, items):
 
 
 def pytest_terminal_summary(terminalreporter):
-    """The bf16 comparisons of the session against the unscaled 2e-2 max-abs
-    bound (the tests apply it on the tensor's scale once max|b| > 1)."""
+    """The bf16 comparisons of the session against the fixed 2e-2 max-abs
+    bound (the tests allow one bf16 ulp of max|b| once that exceeds 2e-2)."""
     _tol = sys.modules.get("_tol")  # the module the tests import (tests/ is on sys.path)
     if _tol is None:
         return
@@ -39,10 +39,11 @@ def pytest_terminal_summary(terminalreporter):
         return
     within = sum(1 for _, mae, _, _ in recs if mae <= _tol.BF16_MAX_ABS)
     tr = terminalreporter
-    tr.write_sep("-", "bf16 parity: unscaled max-abs")
-    tr.write_line(f"{len(recs)} bf16 comparisons; {within} within max-abs {_tol.BF16_MAX_ABS} unscaled; "
+    tr.write_sep("-", "bf16 parity: max-abs against 2e-2")
+    tr.write_line(f"{len(recs)} bf16 comparisons; {within} within max-abs {_tol.BF16_MAX_ABS}; "
                   f"worst rel-L2 {max(r for *_, r in recs):.3e}")
     worst = sorted(recs, key=lambda x: -x[1])[:8]
     for what, mae, mb, r in worst:
-        tr.write_line(f"  {what or '?'}: max-abs {mae:.3e}, max|b| {mb:.3e}, "
-                      f"max-abs/max(1,max|b|) {mae / max(1.0, mb):.3e}, rel-L2 {r:.3e}")
+        ulp = _tol.bf16_ulp(mb)
+        tr.write_line(f"  {what or '?'}: max-abs {mae:.3e} = {mae / ulp if ulp else 0:.2f} ulp of "
+                      f"max|b| {mb:.3e}, rel-L2 {r:.3e}")
