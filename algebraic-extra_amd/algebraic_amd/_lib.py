@@ -94,6 +94,9 @@ SIGNATURES = {
     "algx_gemm_bf16_batched": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                       _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                       _f32, _f32, _p]),
+    "algx_gemm_bf16_splitk_workspace_bytes": (_i64, [_i32, _i32, _i32]),
+    "algx_gemm_bf16_splitk": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i64,
+                                     _i64, _i32, _p]),
     "algx_gemm_bf16_grouped": (_i32, [ctypes.POINTER(GemmBatch), _i32, _i32, _i32, _i32, _f32,
                                       _f32, _p]),
     "algx_qk_prologue_fwd": (_i32, [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,

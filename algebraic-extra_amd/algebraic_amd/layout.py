@@ -14,10 +14,19 @@ last axis and cast to ``dtype`` (bf16 or float32) in one pass; the gradient
 is split and cast back to float32 in one pass. The model's per-step
 compute-dtype copies of the stacked weights for its fused projections.
 
+``project(x, w)``: the model's projection ``x @ w`` (bf16, x (..., din), w
+(din, dout)). Forward and input gradient are plain library GEMMs (hipBLASLt
+through torch); the weight gradient ``x^T dY``, whose K is the batch's token
+count while din x dout is one weight, runs on libalgx's split-K GEMM
+(algx_gemm_bf16_splitk): the library's choice for these shapes leaves most
+of the GPU idle (16 to 84 output tiles of 256 x 256 over 256 compute units).
+
 The first two accept any dtype whose rows (heads_to_tokens: D elements) span a
 multiple of 16 bytes (transpose_last2: 2- or 4-byte elements); all return new
 contiguous tensors.
 """
+
+import math
 
 import ctypes
 
@@ -136,3 +145,60 @@ def concat_cast(parts, dtype: torch.dtype) -> torch.Tensor:
 
 
 __all__ = ["heads_to_tokens", "transpose_last2", "concat_cast"]
+
+
+def splitk_splits(M: int, N: int, K: int) -> int:
+    """Chunks of K for algx_gemm_bf16_splitk: the fewest (a power of two)
+    whose workgroups cover 160 of the 256 compute units, keeping chunks of
+    at least 256 rows that are whole 32-row stages."""
+    tiles = math.ceil(M / 256) * math.ceil(N / 256)
+    s = 1
+    while tiles * s < 160 and K % (64 * s) == 0 and K // (2 * s) >= 256:
+        s *= 2
+    return s
+
+
+def weight_grad(x2: torch.Tensor, g2: torch.Tensor) -> torch.Tensor:
+    """x2^T g2 in bf16 for x2 (T, din), g2 (T, dout) bf16: float32 sums of
+    split-K chunks added in chunk order (algx_gemm_bf16_splitk)."""
+    T, din = x2.shape
+    dout = g2.shape[1]
+    x2, g2 = _contig16(x2), _contig16(g2)
+    splits = splitk_splits(din, dout, T)
+    ws = torch.empty(_lib.query("algx_gemm_bf16_splitk_workspace_bytes", din, dout, splits),
+                     dtype=torch.uint8, device=x2.device)
+    out = torch.empty((din, dout), dtype=torch.bfloat16, device=x2.device)
+    _lib.call("algx_gemm_bf16_splitk", _lib.ptr(x2), _lib.ptr(g2), _lib.ptr(out), _lib.ptr(ws),
+              din, dout, T, 0, 0, din, dout, dout, splits, _lib.stream())
+    return out
+
+
+class _Project(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w):
+        ctx.save_for_backward(x, w)
+        return x @ w
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w = ctx.saved_tensors
+        din, dout = w.shape
+        g = g.contiguous()
+        dx = g @ w.t() if ctx.needs_input_grad[0] else None
+        dw = None
+        if ctx.needs_input_grad[1]:
+            dw = weight_grad(x.reshape(-1, din), g.reshape(-1, dout))
+        return dx, dw
+
+
+def project(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x @ w with the weight gradient on the split-K GEMM (bf16, sizes whole
+    multiples of 8 and a token count of whole 32-row stages); other inputs
+    take torch's product and its autodiff."""
+    din, dout = w.shape
+    T = x.numel() // din if din else 0
+    if (x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or not x.is_cuda
+            or din % 8 or dout % 8 or T % 32 or T == 0):
+        return x @ w
+    return _Project.apply(x, w)
+

@@ -9,7 +9,8 @@ run as HIP kernels of libalgx.so: attention (``flash_attention``, both
 product (and SwiGLU's), the attention prologue (QK-norm, rotation and the
 layout change in one pass, for 64-wide heads) and, with
 ``head_impl="fused"``, the LM head + loss. The projections are plain bf16
-GEMMs (hipBLASLt through torch), with q/k/v and gate/up each fused into one
+GEMMs (hipBLASLt through torch; their weight gradients on libalgx's split-K
+GEMM), with q/k/v and gate/up each fused into one
 GEMM whose joined bf16 weights are cast once per step (libalgx concat_cast),
 and the attention output's head-to-token layout change is a libalgx pass; the
 rotation tables, the dense head and, for other head widths, the rotate-half
@@ -32,7 +33,7 @@ from .kernels.flash import flash_attention
 from .kernels.fused_head import fused_head
 from .kernels.prologue import attention_prologue
 from .kernels.qk_norm import qk_rms_norm
-from .layout import concat_cast, heads_to_tokens
+from .layout import concat_cast, heads_to_tokens, project
 
 F32 = torch.float32
 _DTYPES = {"bfloat16": torch.bfloat16, "float32": torch.float32}
@@ -273,7 +274,7 @@ def _qkv(cfg: LMConfig, cos, sin, h, lp):
     H, D = cfg.n_heads, cfg.head_dim
     dt = h.dtype
     if D == 64:
-        qkv = h @ lp["w_qkv"]
+        qkv = project(h, lp["w_qkv"])
         gains = (lp["q_gain"], lp["k_gain"]) if cfg.qk_norm else (None, None)
         tabs = (None, None) if cfg.pos == "none" else (cos, sin)
         return attention_prologue(qkv, H, gains[0], gains[1], tabs[0], tabs[1], cfg.eps)
@@ -312,14 +313,14 @@ def _block(cfg: LMConfig, cos, sin, x, r, lp):
     else:
         sink = None
     a = heads_to_tokens(_attention(q, k, v, sink, cfg))
-    x, h2 = _add_norm(x, a @ lp["w_o_c"], lp.get("ln2"), cfg)
+    x, h2 = _add_norm(x, project(a, lp["w_o_c"]), lp.get("ln2"), cfg)
     if cfg.ffn not in ("swiglu", "alu_glu"):
         raise ValueError(f"unknown ffn {cfg.ffn!r}")
     # gate and up from one GEMM against [w_g | w_u]; the gated product reads
     # its rows in place and returns the gradient packed the same way.
-    gu = h2 @ lp["w_gu"]
+    gu = project(h2, lp["w_gu"])
     y = glu_packed(gu, "alu" if cfg.ffn == "alu_glu" else "silu", cfg.alu_beta)
-    return x, y @ lp["w_d_c"]
+    return x, project(y, lp["w_d_c"])
 
 
 def _joined(parts, dt):

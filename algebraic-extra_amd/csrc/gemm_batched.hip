@@ -192,6 +192,78 @@ BatchFn pick_batched(bool akc, bool bkc, bool dma, bool sym) {
   return dma ? pick_batched_as<true, false>(akc, bkc) : pick_batched_as<false, false>(akc, bkc);
 }
 
+// Split-K product (the weight gradients of the model's projections, K = the
+// token count): C[m][n] = cast(sum_k opA(m, k) opB(n, k)) with K cut into
+// `splits` chunks of Kc. Workgroup b forms chunk b / ntiles of tile
+// b % ntiles (256 x 256, m along the core's M axis, so a lane's sixteen
+// accumulators are sixteen rows of one column and each store instruction
+// covers 32 consecutive columns of two rows) and stores it in float32 to the
+// chunk's slice of the workspace; a second pass adds the slices in chunk
+// order and casts (so the result does not depend on workgroup timing).
+struct SplitK {
+  const bf16* A;
+  const bf16* B;
+  float* P;  // workspace: splits x M x N float32
+  int64_t lda, ldb;
+  int M, N, Kc, splits, tiles_n;
+};
+
+template <bool AKC, bool BKC, bool DMA>
+__global__ __launch_bounds__(kThreads) void splitk_gemm_kernel(SplitK p) {
+  GEMM_LDS_STAGES;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, c32 = lane & 31;
+  const int wm = w / NWN, wn = w % NWN;
+  const int ntiles = (int)gridDim.x / p.splits;
+  const int split = (int)blockIdx.x / ntiles, tile = (int)blockIdx.x % ntiles;
+  const int m0 = (tile / p.tiles_n) * BM, n0 = (tile % p.tiles_n) * BN;
+  const int64_t k0 = (int64_t)split * p.Kc;
+  const Operand Aop{p.A + (AKC ? k0 : k0 * p.lda), p.lda, p.M, p.Kc};
+  const Operand Bop{p.B + (BKC ? k0 : k0 * p.ldb), p.ldb, p.N, p.Kc};
+  Acc acc;
+  if constexpr (DMA)
+    gemm_tile_dma<AKC, BKC>(Aop, Bop, m0, n0, ring, acc, tid);
+  else
+    gemm_tile<AKC, BKC>(Aop, Bop, m0, n0, s0, s0 + 2 * kStageElems, acc, tid);
+  // acc.v[i][j][r] = partial C[m0 + WTM wm + 32 i + 8 (r / 4) + 4 g + r % 4][n0 + WTN wn + 32 j + c32]
+  float* P = p.P + (int64_t)split * p.M * p.N;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int n = n0 + WTN * wn + 32 * j + c32;
+    if (n >= p.N) continue;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + WTM * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (m < p.M) P[(int64_t)m * p.N + n] = acc.v[i][j][r];
+      }
+  }
+}
+
+// C[m][n] = cast(sum over the chunks of P[s][m][n]), four columns a thread.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ P,
+                                                            bf16* __restrict__ C, int M, int N,
+                                                            int64_t ldc, int splits) {
+  const int64_t mn = (int64_t)M * N;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x * 4;
+  for (int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; e < mn; e += stride) {
+    f32x4 v = *reinterpret_cast<const f32x4*>(P + e);
+    for (int sp = 1; sp < splits; ++sp) {
+      const f32x4 u = *reinterpret_cast<const f32x4*>(P + sp * mn + e);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] += u[c];
+    }
+    const int64_t m = e / N, n = e % N;
+    *reinterpret_cast<bf16x4*>(C + m * ldc + n) = bf16x4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+  }
+}
+
+typedef void (*SplitFn)(SplitK);
+template <bool DMA> SplitFn pick_splitk_as(bool akc, bool bkc) {
+  if (akc) return bkc ? splitk_gemm_kernel<true, true, DMA> : splitk_gemm_kernel<true, false, DMA>;
+  return bkc ? splitk_gemm_kernel<false, true, DMA> : splitk_gemm_kernel<false, false, DMA>;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // Checks one batch's arguments and fills its descriptor (tile counts are set
@@ -306,6 +378,49 @@ extern "C" int32_t algx_gemm_bf16_batched(const void* A, const void* B, const vo
                           stride_a, stride_b, stride_d, stride_c};
   return launch_groups(&g, 1, a_kc != 0, b_kc != 0, symmetric != 0, alpha, beta,
                        (hipStream_t)stream);
+}
+
+extern "C" int64_t algx_gemm_bf16_splitk_workspace_bytes(int32_t M, int32_t N,
+                                                        int32_t splits) {
+  if (M <= 0 || N <= 0 || splits <= 0) return 0;
+  return (int64_t)splits * M * N * (int64_t)sizeof(float);
+}
+
+extern "C" int32_t algx_gemm_bf16_splitk(const void* A, const void* B, void* C, void* workspace,
+                                         int32_t M, int32_t N, int32_t K, int32_t a_kc,
+                                         int32_t b_kc, int64_t lda, int64_t ldb, int64_t ldc,
+                                         int32_t splits, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return fail("gemm_bf16_splitk: negative size");
+  if (splits < 1 || splits > 1024) return fail("gemm_bf16_splitk: splits must be in 1 .. 1024");
+  if (M == 0 || N == 0) return 0;
+  if (A == nullptr || B == nullptr || C == nullptr || workspace == nullptr)
+    return fail("gemm_bf16_splitk: null pointer");
+  if (K == 0 || K % splits) return fail("gemm_bf16_splitk: K must be a positive multiple of splits");
+  const int Kc = K / splits;
+  if (M % 8 || N % 8 || Kc % 8)
+    return fail("gemm_bf16_splitk: M, N and K / splits must be multiples of 8");
+  if (lda % 8 || ldb % 8 || ldc % 8)
+    return fail("gemm_bf16_splitk: leading dimensions must be multiples of 8");
+  if (!aligned16(A) || !aligned16(B) || !aligned16(C) || !aligned16(workspace))
+    return fail("gemm_bf16_splitk: operands must be 16-byte aligned");
+  if (lda < (a_kc ? K : M) || ldb < (b_kc ? K : N) || ldc < N)
+    return fail("gemm_bf16_splitk: leading dimension below the row length");
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int64_t grid = (int64_t)tiles_m * tiles_n * splits;
+  if (grid > 0x7fffffff) return fail("gemm_bf16_splitk: too many tiles");
+  hipStream_t s = (hipStream_t)stream;
+  const SplitK p{(const bf16*)A, (const bf16*)B, (float*)workspace, lda, ldb, M, N, Kc, splits,
+                 tiles_n};
+  const bool dma = Kc % BK == 0;
+  SplitFn fn = dma ? pick_splitk_as<true>(a_kc != 0, b_kc != 0)
+                   : pick_splitk_as<false>(a_kc != 0, b_kc != 0);
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(kThreads), 0, s, p);
+  if (int32_t rc = check_launch("gemm_bf16_splitk")) return rc;
+  int64_t nb = ((int64_t)M * N / 4 + 255) / 256;
+  if (nb > 4096) nb = 4096;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)nb), dim3(256), 0, s,
+                     (const float*)workspace, (bf16*)C, M, N, (int64_t)ldc, splits);
+  return check_launch("gemm_bf16_splitk_reduce");
 }
 
 extern "C" int32_t algx_gemm_bf16_grouped(const algx_gemm_batch* groups, int32_t ngroups,

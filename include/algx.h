@@ -361,6 +361,21 @@ int32_t algx_gemm_bf16_batched(const void* A, const void* B, const void* D, void
                                int64_t ldd, int64_t ldc, int64_t stride_a, int64_t stride_b,
                                int64_t stride_d,
                                int64_t stride_c, float alpha, float beta, void* stream);
+/* algx_gemm_bf16_splitk: the weight gradients of the model's projections
+ * (autodiff of `h @ w` at src/algebraic/model.py:166-191: dW = h^T dY, a
+ * product whose K is the batch's token count while M x N is one weight):
+ *   C[m][n] = cast_bf16(sum_k opA(m, k) opB(n, k))
+ * with opA, opB as in algx_gemm_bf16_batched (a_kc / b_kc, lda / ldb), C
+ * bf16 row-major with ldc. K is cut into `splits` equal chunks formed by
+ * separate workgroups into float32 slices of the workspace
+ * (algx_gemm_bf16_splitk_workspace_bytes(M, N, splits)), which a second
+ * launch adds in chunk order and casts. M, N and K / splits multiples of 8,
+ * leading dimensions multiples of 8, pointers 16-byte aligned,
+ * 1 <= splits <= 1024. */
+int64_t algx_gemm_bf16_splitk_workspace_bytes(int32_t M, int32_t N, int32_t splits);
+int32_t algx_gemm_bf16_splitk(const void* A, const void* B, void* C, void* workspace, int32_t M,
+                              int32_t N, int32_t K, int32_t a_kc, int32_t b_kc, int64_t lda,
+                              int64_t ldb, int64_t ldc, int32_t splits, void* stream);
 /* algx_gemm_bf16_grouped: up to 4 batches of algx_gemm_bf16_batched products
  * in one launch (the operands, sizes and strides of each group its own; the
  * operand layouts, symmetry and alpha/beta shared). Muon orthogonalises

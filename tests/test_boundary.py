@@ -134,6 +134,29 @@ def test_noalloc_forward_rejects_sizes_beyond_its_scratch(monkeypatch):
         assert rc != 0 and b"null pointer" in lib.algx_last_error()
 
 
+def test_splitk_gemm_validation_without_a_gpu():
+    """algx_gemm_bf16_splitk checks its sizes, chunking and alignment before
+    it launches; an empty product launches nothing."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    assert lib.algx_gemm_bf16_splitk_workspace_bytes(1024, 3072, 4) == 4 * 1024 * 3072 * 4
+    assert lib.algx_gemm_bf16_splitk(None, None, None, None, 0, 64, 64, 1, 1, 64, 64, 64, 4,
+                                     None) == 0
+    rc = lib.algx_gemm_bf16_splitk(p, p, p, p, 64, 64, 64, 1, 1, 64, 64, 64, 0, None)
+    assert rc != 0 and b"splits" in lib.algx_last_error()
+    rc = lib.algx_gemm_bf16_splitk(p, p, p, p, 64, 64, 96, 1, 1, 96, 96, 64, 5, None)
+    assert rc != 0 and b"multiple of splits" in lib.algx_last_error()
+    rc = lib.algx_gemm_bf16_splitk(p, p, p, p, 64, 64, 64, 1, 1, 64, 64, 64, 16, None)
+    assert rc != 0 and b"multiples of 8" in lib.algx_last_error()
+    rc = lib.algx_gemm_bf16_splitk(p, ctypes.c_void_p(264), p, p, 64, 64, 64, 1, 1, 64, 64, 64, 2,
+                                   None)
+    assert rc != 0 and b"16-byte aligned" in lib.algx_last_error()
+    rc = lib.algx_gemm_bf16_splitk(p, p, p, p, 64, 64, 64, 1, 1, 32, 64, 64, 2, None)
+    assert rc != 0 and b"leading dimension" in lib.algx_last_error()
+    rc = lib.algx_gemm_bf16_splitk(p, p, p, None, 64, 64, 64, 1, 1, 64, 64, 64, 2, None)
+    assert rc != 0 and b"null pointer" in lib.algx_last_error()
+
+
 def test_grouped_gemm_validation_without_a_gpu():
     """algx_gemm_bf16_grouped checks the group count and every group's
     arguments before it launches; empty groups launch nothing."""

@@ -172,3 +172,71 @@ def test_newton_schulz_groups_in_lockstep_equal_separate_runs():
     together = O._ns_iterate_many([X.clone() for X in Xs], 5)
     for X, got in zip(Xs, together):
         assert torch.equal(got, O._ns_iterate(X.clone(), 5))
+
+
+def _splitk(A, B, a_kc, b_kc, splits):
+    from algebraic_amd import _lib
+    M = A.shape[0] if a_kc else A.shape[1]
+    K = A.shape[1] if a_kc else A.shape[0]
+    N = B.shape[0] if b_kc else B.shape[1]
+    C = torch.full((M, N), float("nan"), device=DEV, dtype=torch.bfloat16)
+    ws = torch.full((_lib.query("algx_gemm_bf16_splitk_workspace_bytes", M, N, splits) // 4,),
+                    float("nan"), device=DEV)
+    _lib.call("algx_gemm_bf16_splitk", _lib.ptr(A), _lib.ptr(B), _lib.ptr(C), _lib.ptr(ws), M, N,
+              K, int(a_kc), int(b_kc), A.shape[1], B.shape[1], N, splits, _lib.stream())
+    return C
+
+
+@pytest.mark.parametrize("a_kc,b_kc", [(True, True), (True, False), (False, True), (False, False)])
+@pytest.mark.parametrize("M,N,K,splits", [(264, 520, 1024, 4), (1024, 1024, 4096, 16),
+                                          (40, 8, 96, 4), (520, 264, 2048, 1), (256, 768, 640, 5)])
+def test_splitk_gemm_matches_float32(a_kc, b_kc, M, N, K, splits):
+    """algx_gemm_bf16_splitk: bf16(opA opB^T) from float32 sums over K cut into
+    chunks (direct-to-LDS stages when a chunk is whole 32-row stages,
+    register-staged otherwise; ragged tiles; every operand layout), into
+    outputs and a workspace that start as NaN; two calls agree bit for bit."""
+    g = torch.Generator(device=DEV).manual_seed(M * 3 + N + K + splits)
+    A = torch.randn((M, K) if a_kc else (K, M), generator=g, device=DEV).bfloat16()
+    B = torch.randn((N, K) if b_kc else (K, N), generator=g, device=DEV).bfloat16()
+    C = _splitk(A, B, a_kc, b_kc, splits)
+    a = A.float() if a_kc else A.float().t()
+    b = B.float() if b_kc else B.float().t()
+    want = a @ b.t()
+    assert torch.isfinite(C.float()).all()
+    err = (C.float() - want).abs()
+    # one bf16 rounding of float32 sums of exact bf16 products
+    assert (err <= 2 ** -8 * want.abs() + 5e-5 * (a.abs() @ b.abs().t())).all(), err.max().item()
+    assert torch.equal(C, _splitk(A, B, a_kc, b_kc, splits))
+
+
+def test_splitk_gemm_rejects_bad_arguments():
+    from algebraic_amd import _lib
+    A = torch.zeros((64, 64), device=DEV, dtype=torch.bfloat16)
+    ws = torch.zeros(64 * 64 * 16, device=DEV)
+    for splits, msg in ((0, "splits"), (3, "multiple of splits"), (16, "multiples of 8")):
+        with pytest.raises(RuntimeError, match=msg):
+            _lib.call("algx_gemm_bf16_splitk", _lib.ptr(A), _lib.ptr(A), _lib.ptr(A), _lib.ptr(ws),
+                      64, 64, 64, 1, 1, 64, 64, 64, splits, _lib.stream())
+
+
+def test_project_gradients_match_torch():
+    """layout.project (the model's projections): forward and input gradient
+    are torch's product; the weight gradient (split-K, float32 sums rounded
+    once to bf16) matches torch's bf16 autodiff within one bf16 rounding."""
+    from algebraic_amd.layout import project
+    g = torch.Generator(device=DEV).manual_seed(11)
+    for (B, T, din, dout) in ((2, 1024, 1024, 3072), (1, 4096, 2688, 1024), (3, 160, 256, 264)):
+        x = torch.randn((B, T, din), generator=g, device=DEV).bfloat16().requires_grad_(True)
+        w = (0.02 * torch.randn((din, dout), generator=g, device=DEV)).bfloat16().requires_grad_(True)
+        dy = torch.randn((B, T, dout), generator=g, device=DEV).bfloat16()
+        out = project(x, w)
+        dx, dw = torch.autograd.grad(out, (x, w), dy)
+        xr, wr = x.detach().clone().requires_grad_(True), w.detach().clone().requires_grad_(True)
+        ref = xr @ wr
+        rdx, rdw = torch.autograd.grad(ref, (xr, wr), dy)
+        assert torch.equal(out, ref)
+        assert (dx.float() - rdx.float()).abs().max().item() <= 2 ** -7 * rdx.float().abs().max().item()
+        want = x.detach().float().reshape(-1, din).t() @ dy.float().reshape(-1, dout)
+        err = (dw.float() - want).abs().max().item()
+        assert err <= 2 ** -7 * want.abs().max().item(), err
+        assert (rdw.float() - want).abs().max().item() <= 2 ** -7 * want.abs().max().item()
