@@ -278,9 +278,9 @@ def _qkv(cfg: LMConfig, cos, sin, h, lp):
         gains = (lp["q_gain"], lp["k_gain"]) if cfg.qk_norm else (None, None)
         tabs = (None, None) if cfg.pos == "none" else (cos, sin)
         return attention_prologue(qkv, H, gains[0], gains[1], tabs[0], tabs[1], cfg.eps)
-    q = (h @ lp["w_q"].to(dt)).view(B, T, H, D).transpose(1, 2)
-    k = (h @ lp["w_k"].to(dt)).view(B, T, H, D).transpose(1, 2)
-    v = (h @ lp["w_v"].to(dt)).view(B, T, H, D).transpose(1, 2)
+    q = project(h, lp["w_q"].to(dt)).view(B, T, H, D).transpose(1, 2)
+    k = project(h, lp["w_k"].to(dt)).view(B, T, H, D).transpose(1, 2)
+    v = project(h, lp["w_v"].to(dt)).view(B, T, H, D).transpose(1, 2)
     if cfg.qk_norm:
         q = _qk_norm(q, lp["q_gain"], cfg)
         k = _qk_norm(k, lp["k_gain"], cfg)
