@@ -10,12 +10,14 @@
 // LDS read through transposing LDS reads in the k-slot order the accumulator
 // layout implies.
 //
-// Software pipeline: the score MFMAs of tile j+1 are issued before the VALU
-// transform of tile j, so the MFMA pipe works while the VALU (the bound of
-// this kernel: about eight VALU operations and one reciprocal square root per
-// score against 256 MFMA flops) runs. K therefore lives one tile ahead of V
-// in a two-buffer LDS ring: iteration j reads K_{j+1} and V_j and fills
-// K_{j+2} and V_{j+1}.
+// Occupancy rather than software pipelining: each wave forms a tile's
+// scores, weights and PV products in order, in at most 128 VGPRs, so four
+// workgroups (32 KB of LDS each) run per CU and four waves per SIMD cover each
+// other's MFMA, LDS and barrier waits while the VALU (the bound of this
+// kernel: about eight VALU operations and one reciprocal square root per score
+// against 256 MFMA flops) works. K and V tiles share a two-slot LDS ring:
+// step j reads slot j % 2, and after the step's barrier the slot takes
+// K_{j+2} and V_{j+2}.
 #include <type_traits>
 
 #include "attn_mfma.h"
@@ -24,7 +26,7 @@ namespace algx {
 namespace mfma {
 namespace {
 
-template <int MODE, bool FAST, bool BOUNDED, int L2N, bool POLY>
+template <int MODE, bool FAST, bool BOUNDED, int L2N, bool POLY, bool EARLY_QS>
 __device__ __forceinline__ void fwd_body(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
@@ -48,9 +50,9 @@ __device__ __forceinline__ void fwd_body(
     for (int ks = 0; ks < 4; ++ks)
       qreg[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks);
   }
-  // The pre-scale's q_s and the guard's partial maxima are stored at the end
-  // of the kernel: a store issued before the K/V prologue would make its
-  // vmcnt wait also wait for the store to land.
+  // The pre-scale's q_s and the guard's partial maxima are stored after the
+  // K/V prologue: a store issued before it would make its vmcnt wait also
+  // wait for the store to land.
   float part_out = 0.0f;
   if (prep.q_s != nullptr) {
     // Fused pre-scale: `q` is the raw query; q_s = cast(q * scale)
@@ -114,8 +116,8 @@ __device__ __forceinline__ void fwd_body(
   zero16(oacc[0]);
   zero16(oacc[1]);
 
-  // K and V tiles move straight from global memory into three-slot LDS rings
-  // (tile t in slot t % 3), unpadded rows with chunk c of row r at chunk
+  // K and V tiles move straight from global memory into two-slot LDS rings
+  // (tile t in slot t % 2), unpadded rows with chunk c of row r at chunk
   // c ^ sw16(r). Each wave issues two 1 KB blocks of each tile (rows 16w ..
   // 16w + 15): lane i of block b fills row 8b + i / 8, physical chunk i % 8,
   // so it reads logical chunk (i % 8) ^ sw16(row) from global memory.
@@ -129,29 +131,41 @@ __device__ __forceinline__ void fwd_body(
   const unsigned wblk = 2048u * (unsigned)__builtin_amdgcn_readfirstlane(w);
   auto issue_k = [&](int t) {
     const bf16* src = k + base + (int64_t)t * FBN * HD;
-    const unsigned dst = lds_u32(Kr[t % 3]) + wblk;
+    const unsigned dst = lds_u32(Kr[t % 2]) + wblk;
     dma16_s(src, voff[0], dst);
     dma16_s(src, voff[1], dst + 1024);
   };
   auto issue_v = [&](int t) {
     const bf16* src = v + base + (int64_t)t * FBN * HD;
-    const unsigned dst = lds_u32(Vr[t % 3]) + wblk;
+    const unsigned dst = lds_u32(Vr[t % 2]) + wblk;
     dma16_s(src, voff[0], dst);
     dma16_s(src, voff[1], dst + 1024);
   };
 
-  // Prologue: K_0..K_2 and V_0, V_1 resident; scores of tile 0; then K_3 and
-  // V_2 issued (K_3 replaces K_0). From then on the end of step kb issues
-  // K_{kb+4} and V_{kb+3} into the slots step kb has finished with, and
-  // waits for K_{kb+2} and V_{kb+1} (issued two steps earlier).
+  // Prologue: K_0, V_0, K_1, V_1 resident (nkb >= 2: a workgroup's own two
+  // diagonal tiles). The end of step kb waits for K_{kb+1} and V_{kb+1}
+  // (issued one step earlier), and after its barrier issues K_{kb+2} and
+  // V_{kb+2} into slot kb % 2, which every wave has finished reading.
 #pragma unroll
-  for (int t = 0; t < 3; ++t)
-    if (t < nkb) issue_k(t);
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-    if (t < nkb) issue_v(t);
+  for (int t = 0; t < 2; ++t) {
+    issue_k(t);
+    issue_v(t);
+  }
   wait_vmcnt<0>();
   __syncthreads();
+  // q_s and the guard's partial maxima go out after the prologue's wait, so
+  // that wait does not cover them; they land during step 0, whose own wait
+  // does. (Two-variant kernels store them at the end instead: there the
+  // early store's addresses raise the scalar register count past its limit.)
+  auto store_prep = [&] {
+    if (prep.q_s != nullptr) {
+      bf16* qsp = prep.q_s + base + (int64_t)qrow * HD + 8 * g;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) *reinterpret_cast<bf16x8*>(qsp + 16 * ks) = qreg[ks];
+      if (prep.partial != nullptr && tid < 3) prep.partial[(int64_t)bid * 3 + tid] = part_out;
+    }
+  };
+  if (EARLY_QS) store_prep();
 
   // A operand of S^T: lane reads K[32 mt + c32][16 ks + 8 g ..] (rows 32 mt
   // apart share the chunk placement).
@@ -159,7 +173,7 @@ __device__ __forceinline__ void fwd_body(
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) koff[ks] = c32 * HD + 8 * ((2 * ks + g) ^ sw16(c32));
   auto scores = [&](int kb, f32x16 (&s)[2]) {
-    const bf16* Kt = Kr[kb % 3];
+    const bf16* Kt = Kr[kb % 2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       zero16(s[mt]);
@@ -259,7 +273,7 @@ __device__ __forceinline__ void fwd_body(
     // key 16kc + 8(s/4) + 4g + s%4 (the accumulator rows the lane owns); the
     // V^T operand is read from the row-major V tile with two transposing
     // reads whose row order matches.
-    const bf16* Vt = Vr[kb % 3];
+    const bf16* Vt = Vr[kb % 2];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       const int mt = kc >> 1, rr = 8 * (kc & 1);
@@ -276,55 +290,32 @@ __device__ __forceinline__ void fwd_body(
   };
 
   auto visible = [&](int kb) { return kb < nkb && kb * FBN <= qw + 31; };
-  auto step = [&](int kb, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
-    const bool vis_next = visible(kb + 1), vis = visible(kb);
-    const bool diag = kb * FBN + FBN - 1 > qw;
-    if (vis_next && vis && !diag) {
-      // Common case in one basic block, with the next tile's score MFMAs
-      // and this tile's PV MFMAs spread through the weight math (one MFMA
-      // per 20, then per 8, VALU operations) instead of issued back to back.
-      scores(kb + 1, nxt);
-      consume(std::false_type{}, kb, cur);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 20, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-      }
-    } else {
-      if (vis_next) scores(kb + 1, nxt);
-      if (vis) {
-        if (diag)
-          consume(std::true_type{}, kb, cur);
-        else
-          consume(std::false_type{}, kb, cur);
-      }
-    }
-    // K_{kb+2} and V_{kb+1} (for step kb + 1) are this wave's loads issued
-    // before the last batch, K_{kb+3} and V_{kb+2}.
-    if (kb + 3 < nkb)
-      wait_vmcnt<4>();
-    else if (kb + 2 < nkb)
-      wait_vmcnt<2>();
-    else
-      wait_vmcnt<0>();
+  // Tiles below the workgroup's first query row: no mask and no branch. The
+  // next tiles' loads are issued after the barrier, so every wave's only
+  // outstanding memory operations at the wait are the previous step's loads.
+  const int nfull = q0 / FBN;
+  for (int kb = 0; kb < nfull; ++kb) {
+    f32x16 sc[2];
+    scores(kb, sc);
+    consume(std::false_type{}, kb, sc);
+    wait_vmcnt<0>();
     __syncthreads();
-    if (kb + 4 < nkb) issue_k(kb + 4);
-    if (kb + 3 < nkb) issue_v(kb + 3);
-  };
-
-  f32x16 sa[2], sb[2];
-  scores(0, sa);
-  __syncthreads();  // every wave has read K_0, whose slot takes K_3
-  if (3 < nkb) issue_k(3);
-  if (2 < nkb) issue_v(2);
-  for (int kb = 0; kb < nkb; kb += 2) {
-    step(kb, sa, sb);
-    if (kb + 1 < nkb) step(kb + 1, sb, sa);
+    issue_k(kb + 2);
+    issue_v(kb + 2);
+  }
+  // The workgroup's two diagonal tiles (nkb = nfull + 2), already loaded or
+  // in flight; a wave skips the tiles wholly above its own rows.
+  for (int kb = nfull; kb < nkb; ++kb) {
+    f32x16 sc[2];
+    if (visible(kb)) {
+      scores(kb, sc);
+      if (kb * FBN + FBN - 1 > qw)
+        consume(std::true_type{}, kb, sc);
+      else
+        consume(std::false_type{}, kb, sc);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
   }
 
   const float l_tot = l_row + __shfl_xor(l_row, 32, 64);
@@ -344,12 +335,7 @@ __device__ __forceinline__ void fwd_body(
         *reinterpret_cast<f32x4*>(o_precise + orow + d) = val;
     }
   if (g == 0) stat[(int64_t)bh * T_ + qrow] = final_stat(var, m_row, l_tot);
-  if (prep.q_s != nullptr) {
-    bf16* qsp = prep.q_s + base + (int64_t)qrow * HD + 8 * g;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) *reinterpret_cast<bf16x8*>(qsp + 16 * ks) = qreg[ks];
-    if (prep.partial != nullptr && tid < 3) prep.partial[(int64_t)bid * 3 + tid] = part_out;
-  }
+  if (!EARLY_QS) store_prep();
   if (prep.dq_zero != nullptr) {
     // The workgroup's 128 query rows of the accumulator are one contiguous
     // 32 KB run: eight coalesced 16-byte stores per thread.
@@ -359,22 +345,35 @@ __device__ __forceinline__ void fwd_body(
   }
 }
 
+// Four workgroups per CU (four waves per SIMD, at most 128 VGPRs) for the
+// single variants whose body fits that budget; three (168 VGPRs) for those
+// that would spill at 128: the runtime power loop (n outside 8..32), the
+// polynomial radical, the clamped (unbounded) unshifted weights other than
+// the fast radical at n = 8 or 16, and the two-variant guarded kernels.
+constexpr int fwd_blocks_per_cu(int lo, int hi) {
+  return lo != hi || cfg_l2n(lo) == 0 || cfg_poly(lo) ||
+                 (cfg_mode(lo) == MODE_NOSHIFT && !cfg_bounded(lo) &&
+                  (!cfg_fast(lo) || cfg_l2n(lo) == 5))
+             ? 3
+             : 4;
+}
+
 // The guard word (if any) picks the low or the high variant for the whole
 // grid, mirroring lax.cond(in_range, low, high).
 template <int LO, int HI>
-__global__ __launch_bounds__(256, 2) void fwd_mfma_kernel(
+__global__ __launch_bounds__(256, fwd_blocks_per_cu(LO, HI)) void fwd_mfma_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
     float* __restrict__ stat, int H, int T_, KVariant lo, KVariant hi,
     const int32_t* __restrict__ guard, FwdPrep prep) {
-  __shared__ __attribute__((aligned(16))) bf16 Kr[3][FBN * HD];
-  __shared__ __attribute__((aligned(16))) bf16 Vr[3][FBN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 Kr[2][FBN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 Vr[2][FBN * HD];
   __shared__ float red[3][4];
   if (LO == HI || guard_in_range(guard))
-    fwd_body<cfg_mode(LO), cfg_fast(LO), cfg_bounded(LO), cfg_l2n(LO), cfg_poly(LO)>(
+    fwd_body<cfg_mode(LO), cfg_fast(LO), cfg_bounded(LO), cfg_l2n(LO), cfg_poly(LO), LO == HI>(
         q, k, v, sink, o, o_precise, stat, H, T_, lo, prep, Kr, Vr, red, blockIdx.x, gridDim.x);
   else
-    fwd_body<cfg_mode(HI), cfg_fast(HI), cfg_bounded(HI), cfg_l2n(HI), cfg_poly(HI)>(
+    fwd_body<cfg_mode(HI), cfg_fast(HI), cfg_bounded(HI), cfg_l2n(HI), cfg_poly(HI), LO == HI>(
         q, k, v, sink, o, o_precise, stat, H, T_, hi, prep, Kr, Vr, red, blockIdx.x, gridDim.x);
 }
 
@@ -396,8 +395,8 @@ __global__ __launch_bounds__(256, 2) void fwd_fallback_kernel(
     const bf16* __restrict__ q_s, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ sink, bf16* __restrict__ o, float* __restrict__ o_precise,
     float* __restrict__ stat, int H, int T_, KVariant hi, GuardIn gin, int ntiles) {
-  __shared__ __attribute__((aligned(16))) bf16 Kr[3][FBN * HD];
-  __shared__ __attribute__((aligned(16))) bf16 Vr[3][FBN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 Kr[2][FBN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 Vr[2][FBN * HD];
   __shared__ float red[3][4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   float mx[3] = {0.0f, 0.0f, 0.0f};
@@ -435,7 +434,7 @@ __global__ __launch_bounds__(256, 2) void fwd_fallback_kernel(
   if (ok) return;
   for (int b = blockIdx.x; b < ntiles; b += gridDim.x) {
     __syncthreads();  // LDS of the previous tile is no longer read
-    fwd_body<cfg_mode(HI), cfg_fast(HI), cfg_bounded(HI), cfg_l2n(HI), cfg_poly(HI)>(
+    fwd_body<cfg_mode(HI), cfg_fast(HI), cfg_bounded(HI), cfg_l2n(HI), cfg_poly(HI), false>(
         q_s, k, v, sink, o, o_precise, stat, H, T_, hi, FwdPrep{}, Kr, Vr, red, b, ntiles);
   }
 }
