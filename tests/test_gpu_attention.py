@@ -96,6 +96,23 @@ def test_flash_matches_oracle(kind, n, c, with_sink, shift, fast, dtype):
     _check_all(got, want, dtype)
 
 
+@pytest.mark.parametrize("T", [128, 384])
+@pytest.mark.parametrize("kw", [dict(kind="asinh", n=16, c=8.0, range_guard=True),
+                                dict(kind="asinh", n=16, c=16.0, shift=True, fast_rho=True),
+                                dict(kind="softmax")], ids=["guarded", "shift", "softmax"])
+def test_mfma_forward_block_counts(T, kw):
+    """bf16 MFMA kernels at one 128-query block (only the two diagonal key
+    tiles, no unmasked loop) and at an odd block count (the backward's last
+    256-key block half empty), against the oracle."""
+    shape = (1, 2, T, 64)
+    q, k, v, g = _rand(shape, 11 + T)
+    sink = (torch.tensor([0.3, -0.7]).reshape(1, 2, 1, 1)
+            if kw["kind"] == "softmax" else None)
+    got = _run(q, k, v, g, sink, block=128, **kw)
+    want, _ = _oracle(q, k, v, g, sink, "bf16", **kw)
+    _check_all(got, want, "bf16")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("mode", ["root", "inverse", "guarded"])
 def test_model_attention_statistics(mode, dtype):
