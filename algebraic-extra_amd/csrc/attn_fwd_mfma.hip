@@ -293,6 +293,7 @@ __device__ __forceinline__ void fwd_body(
   // Tiles below the workgroup's first query row: no mask and no branch. The
   // next tiles' loads are issued after the barrier, so every wave's only
   // outstanding memory operations at the wait are the previous step's loads.
+  static_assert(FBM == 2 * FBN, "a workgroup's query block spans two key tiles");
   const int nfull = q0 / FBN;
   for (int kb = 0; kb < nfull; ++kb) {
     f32x16 sc[2];
