@@ -300,7 +300,18 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 // load during the previous tile's last stages and epilogue. Several tiles
 // need nk to be a multiple of the ring's stage count (every tile starts at
 // slot 0).
-template <bool AKC, bool BKC, typename Src, typename Epi>
+//
+// Each step's refill (four loads of the stage two ahead) is issued between
+// the MFMAs of the step's second half, not in a burst ahead of them. With
+// STORE_HEAVY false the loop has no branch: a step with nothing to refill (a
+// tile's first step, whose refill ran before the previous epilogue, and the
+// steps past the sequence's end) repeats a load that changes nothing — the
+// stage already in flight into the same slot, or the stage being read into
+// the slot just consumed, which nothing reads again. Kernels whose epilogue
+// stores a whole output tile pass STORE_HEAVY: such a repeated load would
+// queue behind those stores and hold up the next wait, so they skip it with
+// a branch instead.
+template <bool AKC, bool BKC, bool STORE_HEAVY = false, typename Src, typename Epi>
 __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t stepB, int ntiles,
                                                 Src&& src, const DmaRing& ring, Acc& acc,
                                                 int tid, Epi&& epi) {
@@ -392,14 +403,32 @@ __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t s
         const int g = g0 + kk;
         if (!landed) wait_stages(min(g + S - 2, G - 1) - (g + 1));
         asm volatile("s_barrier" ::: "memory");
-        if (kk + S - 1 < nk)
-          issue(sa0, sa1, sb0, sb1, kk + S - 1, refill);
-        else if (t + 1 < ntiles)
-          issue(na0, na1, nb0, nb1, kk + S - 1 - nk, refill);
       }
       rd(nxt, 0, xa, xb);
-      __builtin_amdgcn_sched_barrier(0);
-      mm(ya, yb);
+      // The refill: stage kk + S - 1 of this tile, else of the next tile, else
+      // (past the end) a repeat of stage kk into the slot just consumed.
+      const bool here = kk + S - 1 < nk, next = !here && t + 1 < ntiles;
+      const bool fill = !STORE_HEAVY || (!synced && (here || next));
+      const bf16* p0 = next ? na0 : sa0;
+      const bf16* p1 = next ? na1 : sa1;
+      const bf16* q0 = next ? nb0 : sb0;
+      const bf16* q1 = next ? nb1 : sb1;
+      const int ks = here ? kk + S - 1 : next ? kk + S - 1 - nk : kk;
+      const unsigned dA = lds_addr(refill) + wofs, dB = dA + 2 * kDmaOpElems;
+      int64_t oa = ks * stepA, ob = ks * stepB;
+      asm volatile("" : "+s"(oa), "+s"(ob));
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          acc.v[i][j] = mfma32(ya[i], yb[j], acc.v[i][j]);
+          if (j == TJ - 1 && fill) {
+            if (i == 0) dma16(p0 + oa, dA);
+            if (i == 1) dma16(p1 + oa, dA + 1024);
+            if (i == 2) dma16(q0 + ob, dB);
+            if (i == 3) dma16(q1 + ob, dB + 1024);
+          }
+        }
     };
     // Slots are named statically: S stages a turn.
     for (int kk = 0; kk < nk; kk += S) {
@@ -424,6 +453,10 @@ __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t s
       asm volatile("s_barrier" ::: "memory");
       issue(na0, na1, nb0, nb1, S - 1, ring.slot[S - 1]);
       if (S >= 4) wait_vm<4>();
+    } else if (!STORE_HEAVY) {
+      // The last step's repeated load may still be writing the ring: let it
+      // land before the workgroup can end and its LDS be reassigned.
+      wait_vm<0>();
     }
     epi(t, acc);
     acc.zero();
@@ -436,14 +469,14 @@ __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t s
 
 // Products of `ntiles` output tiles that share the B rows n0: tile t uses A
 // rows m0 + t BM; epi(t, m0 + t BM, acc) receives each finished tile.
-template <bool AKC, bool BKC, typename Epi>
+template <bool AKC, bool BKC, bool STORE_HEAVY = false, typename Epi>
 __device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B, int m0,
                                              int ntiles, int n0, const DmaRing& ring, Acc& acc,
                                              int tid, Epi&& epi) {
   const int w = tid >> 6, lane = tid & 63;
   const bf16* b0 = dma_src<BKC>(B, n0, 2 * w, lane);
   const bf16* b1 = dma_src<BKC>(B, n0, 2 * w + 1, lane);
-  gemm_stream_dma<AKC, BKC>(
+  gemm_stream_dma<AKC, BKC, STORE_HEAVY>(
       A.K / BK, kstep<AKC>(A), kstep<BKC>(B), ntiles,
       [&](int t, const bf16*& a0, const bf16*& a1, const bf16*& sb0, const bf16*& sb1) {
         a0 = dma_src<AKC>(A, m0 + t * BM, 2 * w, lane);

@@ -307,7 +307,8 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
   };
   Acc acc;
   if constexpr (DMA) {
-    gemm_seq_dma<true, true>(A, B, t_begin * BM, t_end - t_begin, n0, ring, acc, tid, emit_tile);
+    gemm_seq_dma<true, true, true>(A, B, t_begin * BM, t_end - t_begin, n0, ring, acc, tid,
+                                   emit_tile);
   } else {
     for (int t = t_begin; t < t_end; ++t) {
       gemm_tile<true, true>(A, B, t * BM, n0, s0, s0 + 2 * kStageElems, acc, tid);
