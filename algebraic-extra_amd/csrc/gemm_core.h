@@ -277,6 +277,18 @@ __device__ __forceinline__ void dma16(const bf16* src, unsigned lds) {
                : "memory", "m0");
 }
 
+// Two LDS-DMA loads of a wave under one M0: the first block's 16-byte lanes
+// go to lds + 16 i, the second's to lds + 1024 + 16 i through the
+// instruction offset, which the global address takes too (so src1m is the
+// second block's source minus 1024 bytes).
+__device__ __forceinline__ void dma16x2(const bf16* src0, const bf16* src1m, unsigned lds) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+      "global_load_lds_dwordx4 %2, off offset:1024" ::"s"(lds),
+      "v"(src0), "v"(src1m)
+      : "memory", "m0");
+}
+
 // s_waitcnt immediates: vmcnt(n) with expcnt and lgkmcnt unconstrained.
 template <int N> __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | N);
@@ -301,8 +313,9 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 // need nk to be a multiple of the ring's stage count (every tile starts at
 // slot 0).
 //
-// Each step's refill (four loads of the stage two ahead) is issued between
-// the MFMAs of the step's second half, not in a burst ahead of them. With
+// Each step's refill (four loads of the stage two ahead, as two pairs that
+// share one M0 write) is issued between the MFMAs of the step's second half,
+// not in a burst ahead of them. With
 // STORE_HEAVY false the loop has no branch: a step with nothing to refill (a
 // tile's first step, whose refill ran before the previous epilogue, and the
 // steps past the sequence's end) repeats a load that changes nothing — the
@@ -423,10 +436,8 @@ __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t s
         for (int j = 0; j < TJ; ++j) {
           acc.v[i][j] = mfma32(ya[i], yb[j], acc.v[i][j]);
           if (j == TJ - 1 && fill) {
-            if (i == 0) dma16(p0 + oa, dA);
-            if (i == 1) dma16(p1 + oa, dA + 1024);
-            if (i == 2) dma16(q0 + ob, dB);
-            if (i == 3) dma16(q1 + ob, dB + 1024);
+            if (i == 1) dma16x2(p0 + oa, p1 + (oa - 512), dA);
+            if (i == 3) dma16x2(q0 + ob, q1 + (ob - 512), dB);
           }
         }
     };
