@@ -26,7 +26,7 @@ def _check(got, want):
 
 @pytest.mark.parametrize("a_kc,b_kc", [(True, True), (True, False), (False, True), (False, False)])
 @pytest.mark.parametrize("batch,M,N,K", [(3, 264, 520, 96), (8, 256, 256, 1024), (2, 40, 8, 72),
-                                         (5, 520, 264, 200)])
+                                         (5, 520, 264, 200), (2, 264, 520, 32), (2, 256, 256, 64)])
 def test_batched_gemm_layouts(a_kc, b_kc, batch, M, N, K):
     """Ragged tiles (M, N not multiples of 256), K a multiple of 32 (direct-to-
     LDS stages) or only of 8 (register-staged stages), batches that do and do
