@@ -315,15 +315,17 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 //
 // Each step's refill (four loads of the stage two ahead, as two pairs that
 // share one M0 write) is issued between the MFMAs of the step's second half,
-// not in a burst ahead of them. With
-// STORE_HEAVY false the loop has no branch: a step with nothing to refill (a
-// tile's first step, whose refill ran before the previous epilogue, and the
-// steps past the sequence's end) repeats a load that changes nothing — the
-// stage already in flight into the same slot, or the stage being read into
-// the slot just consumed, which nothing reads again. Kernels whose epilogue
-// stores a whole output tile pass STORE_HEAVY: such a repeated load would
-// queue behind those stores and hold up the next wait, so they skip it with
-// a branch instead.
+// not in a burst ahead of them. With STORE_HEAVY false the loop has no
+// branch: a step with nothing to refill (a tile's first step, whose refill
+// ran before the previous epilogue, and the steps past the sequence's end)
+// repeats a load that changes nothing: the stage already in flight into the
+// same slot, or the stage being read into the slot just consumed, which
+// nothing reads again. Kernels whose epilogue stores a whole output tile pass
+// STORE_HEAVY: such a repeated load would queue behind those stores and hold
+// up the next wait, so they skip it with a branch instead. A pair's second
+// source is passed 1024 bytes low (src - 512 elements): the instruction
+// offset adds the 1024 bytes back to the global address as it does to the
+// LDS one, so a clamped source (dma_src's op.p) still reads in bounds.
 template <bool AKC, bool BKC, bool STORE_HEAVY = false, typename Src, typename Epi>
 __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t stepB, int ntiles,
                                                 Src&& src, const DmaRing& ring, Acc& acc,
