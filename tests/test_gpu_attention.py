@@ -96,6 +96,21 @@ def test_flash_matches_oracle(kind, n, c, with_sink, shift, fast, dtype):
     _check_all(got, want, dtype)
 
 
+@pytest.mark.parametrize("n", [2, 4, 64])
+@pytest.mark.parametrize("shift", [False, True])
+def test_mfma_runtime_power(n, shift):
+    """bf16 MFMA kernels with n outside 8..32, whose weight takes its n-th
+    power in a runtime loop (the kernels built for three workgroups per CU),
+    forward and backward against the oracle, with a sink."""
+    shape = (1, 2, 256, 64)
+    q, k, v, g = _rand(shape, 40 + n + int(shift))
+    sink = torch.tensor([0.4, -0.3]).reshape(1, 2, 1, 1)
+    kw = dict(kind="asinh", n=n, c=8.0, shift=shift)
+    got = _run(q, k, v, g, sink, block=128, **kw)
+    want, _ = _oracle(q, k, v, g, sink, "bf16", **kw)
+    _check_all(got, want, "bf16")
+
+
 @pytest.mark.parametrize("T", [128, 384])
 @pytest.mark.parametrize("kw", [dict(kind="asinh", n=16, c=8.0, range_guard=True),
                                 dict(kind="asinh", n=16, c=16.0, shift=True, fast_rho=True),
