@@ -29,6 +29,9 @@ __device__ __forceinline__ unsigned lds_u32(const void* p) {
 // byte address lds + 16 i (M0 = the wave-uniform lds). Issued as assembly so
 // that the compiler's wait insertion does not treat every later LDS read as
 // depending on it; callers wait for their loads with explicit vmcnt counts.
+// M0 is set here and named as clobbered; the compiler uses M0 nowhere in the
+// attention kernels (every M0 write in their generated code is one of these
+// loads), so it holds no value of its own there across the statement.
 __device__ __forceinline__ void dma16_s(const void* base, unsigned voff, unsigned lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
                : "memory", "m0");

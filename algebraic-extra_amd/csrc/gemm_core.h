@@ -271,7 +271,11 @@ __device__ __forceinline__ bf16x8 operand_dma(const bf16* tile, int mn0, int k0,
 // track it: its waitcnt pass cannot tell which LDS buffer such a load writes
 // and would wait for all of them before every LDS read; the ring below waits
 // for its own loads explicitly (wait_vm) before the barrier that publishes
-// them.
+// them. The assembly sets M0 itself and names it as clobbered; the compiler
+// treats M0 as reserved and uses it nowhere in these kernels (no indirect
+// register indexing, GWS or compiler-issued LDS DMA: every M0 write in their
+// generated code is one of these loads), so no value of its own lives in M0
+// across the statement.
 __device__ __forceinline__ void dma16(const bf16* src, unsigned lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
                : "memory", "m0");
