@@ -43,6 +43,10 @@ def attn_flops_fwd(B, H, T, D):
     return 4.0 * B * H * T * T * D / 2.0      # causal, bench_attention.py:50
 
 
+def head_flops(N, d, V):
+    return 3 * 2.0 * N * d * V                # logits, dh, dE; bench_head.py:36
+
+
 def make_attention_inputs(B, H, T, D, seed, dev, qk_norm=True):
     """q, k, v (leaves) and dO, bf16 N(0, 1); q and k QK-normalised as the
     model's attention inputs are, or raw N(0, 1) as the reference's harness
@@ -173,7 +177,7 @@ def bench_head(steps, warmup, dev, N=16384, d=768, V=50304, kind="alg_ce", n=8, 
         pr = Probe(name, steps)
         time_steps(step, steps, 1, pr, settle_s=0.0)
         split[{"head_fwd": "fwd_ms", "head_dz": "dz_ms", "head_de": "dh_dE_ms"}[name]] = pr.mean_ms()
-    flops = 3 * 2 * N * d * V
+    flops = head_flops(N, d, V)
     return {"workload": f"N={N},d={d},V={V},{kind} n={n} c={c}", "ms_per_step": dt * 1e3,
             "tokens_per_s": N / dt, "tflops": flops / dt / 1e12,
             "frac": flops / dt / 1e12 / PEAK_BF16_TFLOPS, **split,
