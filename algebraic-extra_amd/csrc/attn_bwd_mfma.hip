@@ -142,14 +142,14 @@ __device__ __forceinline__ void bwd_body(
 
   // B operands: lane holds K[kcol][16ks + 8g ..] and V[kcol][16ks + 8g ..].
   bf16x8 kreg[4], vreg[4];
+  // A wave whose keys lie past T (only in a last, partial key block, which
+  // the diagonal loop handles) never forms scores, so it reads the last row.
+  {
+    const int kc = wave_keys ? kcol : T_ - 1;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    if (wave_keys) {
-      kreg[ks] = *reinterpret_cast<const bf16x8*>(k + base + (int64_t)kcol * HD + 16 * ks + 8 * g);
-      vreg[ks] = *reinterpret_cast<const bf16x8*>(v + base + (int64_t)kcol * HD + 16 * ks + 8 * g);
-    } else {
-      kreg[ks] = bf16x8{};
-      vreg[ks] = bf16x8{};
+    for (int ks = 0; ks < 4; ++ks) {
+      kreg[ks] = *reinterpret_cast<const bf16x8*>(k + base + (int64_t)kc * HD + 16 * ks + 8 * g);
+      vreg[ks] = *reinterpret_cast<const bf16x8*>(v + base + (int64_t)kc * HD + 16 * ks + 8 * g);
     }
   }
   // Ones in the k rows 64, 65 of the extended V^T (dP's -di block).
@@ -157,18 +157,17 @@ __device__ __forceinline__ void bwd_body(
   const bf16x8 ones = g == 0 ? bf16x8{one, one, zero, zero, zero, zero, zero, zero} : bf16x8{};
   const float neg_g0 = g == 0 ? -1.0f : 0.0f;
   // K^T of the workgroup's keys for the dQ product (8 lanes share a key row,
-  // so the global reads coalesce); dS^T buffer 1 starts zeroed because the
-  // first tile's dQ step reads it.
+  // so the global reads coalesce), loaded here and moved to LDS in the
+  // prologue below.
+  constexpr int KT_CHUNKS = BKN * HD / 8 / NTHR;
+  bf16x8 ktv[KT_CHUNKS];
 #pragma unroll
-  for (int i = 0; i < BKN * HD / 8 / NTHR; ++i) {
+  for (int i = 0; i < KT_CHUNKS; ++i) {
     const int c = tid + NTHR * i, row = c >> 3, col = 8 * (c & 7);
-    const bf16x8 val =
-        key0 + row < T_ ? *reinterpret_cast<const bf16x8*>(k + base + (int64_t)(key0 + row) * HD + col)
-                        : bf16x8{};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) L.kt[(col + e) * KTR + row] = val[e];
-    *reinterpret_cast<bf16x4*>(&L.dst[1][row * DSTR + col]) = bf16x4{};
-    *reinterpret_cast<bf16x4*>(&L.dst[1][row * DSTR + col + 4]) = bf16x4{};
+    // rows past T read the last row (zeroed when stored): no branch around
+    // the load
+    const int kr = key0 + row < T_ ? key0 + row : T_ - 1;
+    ktv[i] = *reinterpret_cast<const bf16x8*>(k + base + (int64_t)kr * HD + col);
   }
 
   f32x16 dka[2], dva[2];
@@ -301,15 +300,23 @@ __device__ __forceinline__ void bwd_body(
     }
   };
 
-  // Prologue: tile qt0 into buffer 0, tile qt0+1 in registers; the explicit
-  // drains keep the loop's memory-counter waits from covering prologue loads
-  // (the counter retires in order, so such a wait would also wait for the
-  // dQ atomics issued later in each iteration).
+  // Prologue: every setup load (the wave's K and V rows, the K^T block and
+  // tiles qt0 and qt0+1) is in flight at once, so the setup costs one memory
+  // round trip rather than one per step. K^T, a zeroed dS^T buffer 1 (the
+  // first tile's dQ step reads it) and tile qt0 go to LDS; tile qt0+1 stays
+  // in registers until the first iteration stores it.
   gload(qt0);
-  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+#pragma unroll
+  for (int i = 0; i < KT_CHUNKS; ++i) {
+    const int c = tid + NTHR * i, row = c >> 3, col = 8 * (c & 7);
+    const bf16x8 val = key0 + row < T_ ? ktv[i] : bf16x8{};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) L.kt[(col + e) * KTR + row] = val[e];
+    *reinterpret_cast<bf16x4*>(&L.dst[1][row * DSTR + col]) = bf16x4{};
+    *reinterpret_cast<bf16x4*>(&L.dst[1][row * DSTR + col + 4]) = bf16x4{};
+  }
   lstore(0);
   gload(qt0 + 1 < nqt ? qt0 + 1 : qt0);
-  __builtin_amdgcn_s_waitcnt(kWaitVm0);
   __syncthreads();
 
   // Every iteration has the same memory-operation sequence (dQ atomics of the

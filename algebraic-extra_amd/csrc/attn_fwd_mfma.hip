@@ -42,6 +42,43 @@ __device__ __forceinline__ void fwd_body(
   const int q0 = qb * FBM, qw = q0 + 32 * w, qrow = qw + c32;
   const int log2n = var.log2n;
 
+  // K and V tiles move straight from global memory into two-slot LDS rings
+  // (tile t in slot t % 2), unpadded rows with chunk c of row r at chunk
+  // c ^ sw16(r). Each wave issues two 1 KB blocks of each tile (rows 16w ..
+  // 16w + 15): lane i of block b fills row 8b + i / 8, physical chunk i % 8,
+  // so it reads logical chunk (i % 8) ^ sw16(row) from global memory.
+  const int nkb = (q0 + FBM) / FBN;
+  unsigned voff[2];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+    const int row = 8 * (2 * w + h2) + (lane >> 3);
+    voff[h2] = (unsigned)(row * HD + 8 * ((lane & 7) ^ sw16(row))) * 2u;
+  }
+  const unsigned wblk = 2048u * (unsigned)__builtin_amdgcn_readfirstlane(w);
+  auto issue_k = [&](int t) {
+    const bf16* src = k + base + (int64_t)t * FBN * HD;
+    const unsigned dst = lds_u32(Kr[t % 2]) + wblk;
+    dma16_s(src, voff[0], dst);
+    dma16_s(src, voff[1], dst + 1024);
+  };
+  auto issue_v = [&](int t) {
+    const bf16* src = v + base + (int64_t)t * FBN * HD;
+    const unsigned dst = lds_u32(Vr[t % 2]) + wblk;
+    dma16_s(src, voff[0], dst);
+    dma16_s(src, voff[1], dst + 1024);
+  };
+
+  // Prologue, issued before anything else the workgroup loads: K_0, V_0,
+  // K_1, V_1 resident (nkb >= 2: a workgroup's own two diagonal tiles).
+  // The end of step kb waits for K_{kb+1} and V_{kb+1}
+  // (issued one step earlier), and after its barrier issues K_{kb+2} and
+  // V_{kb+2} into slot kb % 2, which every wave has finished reading.
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    issue_k(t);
+    issue_v(t);
+  }
+
   // B operand of S^T = K Q_s^T: lane holds Q_s[qrow][16*ks + 8*g .. +7].
   bf16x8 qreg[4];
   {
@@ -49,6 +86,17 @@ __device__ __forceinline__ void fwd_body(
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
       qreg[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks);
+  }
+  // The guard's k and v rows (reduced below) are fetched now too, so q, these
+  // rows and the K/V prologue tiles share one memory round trip.
+  bf16x8 kxs[4], vxs[4];
+  if (prep.q_s != nullptr && prep.partial != nullptr) {
+    const int64_t krow = base + (int64_t)(q0 + (tid >> 1)) * HD + 32 * (tid & 1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      kxs[c] = *reinterpret_cast<const bf16x8*>(k + krow + 8 * c);
+      vxs[c] = *reinterpret_cast<const bf16x8*>(v + krow + 8 * c);
+    }
   }
   // The pre-scale's q_s and the guard's partial maxima are stored after the
   // K/V prologue: a store issued before it would make its vmcnt wait also
@@ -76,12 +124,11 @@ __device__ __forceinline__ void fwd_body(
     if (prep.partial != nullptr) {
       auto nan_to_inf = [](float x) { return x != x ? __builtin_inff() : x; };
       sq = nan_to_inf(sq + __shfl_xor(sq, 32, 64));
-      const int64_t krow = base + (int64_t)(q0 + (tid >> 1)) * HD + 32 * (tid & 1);
       float sk = 0.0f, mv = 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const bf16x8 kx = *reinterpret_cast<const bf16x8*>(k + krow + 8 * c);
-        const bf16x8 vx = *reinterpret_cast<const bf16x8*>(v + krow + 8 * c);
+        const bf16x8 kx = kxs[c];
+        const bf16x8 vx = vxs[c];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float kf = (float)kx[e];
@@ -116,41 +163,6 @@ __device__ __forceinline__ void fwd_body(
   zero16(oacc[0]);
   zero16(oacc[1]);
 
-  // K and V tiles move straight from global memory into two-slot LDS rings
-  // (tile t in slot t % 2), unpadded rows with chunk c of row r at chunk
-  // c ^ sw16(r). Each wave issues two 1 KB blocks of each tile (rows 16w ..
-  // 16w + 15): lane i of block b fills row 8b + i / 8, physical chunk i % 8,
-  // so it reads logical chunk (i % 8) ^ sw16(row) from global memory.
-  const int nkb = (q0 + FBM) / FBN;
-  unsigned voff[2];
-#pragma unroll
-  for (int h2 = 0; h2 < 2; ++h2) {
-    const int row = 8 * (2 * w + h2) + (lane >> 3);
-    voff[h2] = (unsigned)(row * HD + 8 * ((lane & 7) ^ sw16(row))) * 2u;
-  }
-  const unsigned wblk = 2048u * (unsigned)__builtin_amdgcn_readfirstlane(w);
-  auto issue_k = [&](int t) {
-    const bf16* src = k + base + (int64_t)t * FBN * HD;
-    const unsigned dst = lds_u32(Kr[t % 2]) + wblk;
-    dma16_s(src, voff[0], dst);
-    dma16_s(src, voff[1], dst + 1024);
-  };
-  auto issue_v = [&](int t) {
-    const bf16* src = v + base + (int64_t)t * FBN * HD;
-    const unsigned dst = lds_u32(Vr[t % 2]) + wblk;
-    dma16_s(src, voff[0], dst);
-    dma16_s(src, voff[1], dst + 1024);
-  };
-
-  // Prologue: K_0, V_0, K_1, V_1 resident (nkb >= 2: a workgroup's own two
-  // diagonal tiles). The end of step kb waits for K_{kb+1} and V_{kb+1}
-  // (issued one step earlier), and after its barrier issues K_{kb+2} and
-  // V_{kb+2} into slot kb % 2, which every wave has finished reading.
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    issue_k(t);
-    issue_v(t);
-  }
   wait_vmcnt<0>();
   __syncthreads();
   // q_s and the guard's partial maxima go out after the prologue's wait, so
