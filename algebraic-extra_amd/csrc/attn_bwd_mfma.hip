@@ -302,9 +302,8 @@ __device__ __forceinline__ void bwd_body(
 
   // Prologue: every setup load (the wave's K and V rows, the K^T block and
   // tiles qt0 and qt0+1) is in flight at once, so the setup costs one memory
-  // round trip rather than one per step. K^T, a zeroed dS^T buffer 1 (the
-  // first tile's dQ step reads it) and tile qt0 go to LDS; tile qt0+1 stays
-  // in registers until the first iteration stores it.
+  // round trip rather than one per step. K^T and tile qt0 go to LDS; tile
+  // qt0+1 stays in registers until the first iteration stores it.
   gload(qt0);
 #pragma unroll
   for (int i = 0; i < KT_CHUNKS; ++i) {
@@ -312,18 +311,16 @@ __device__ __forceinline__ void bwd_body(
     const bf16x8 val = key0 + row < T_ ? ktv[i] : bf16x8{};
 #pragma unroll
     for (int e = 0; e < 8; ++e) L.kt[(col + e) * KTR + row] = val[e];
-    *reinterpret_cast<bf16x4*>(&L.dst[1][row * DSTR + col]) = bf16x4{};
-    *reinterpret_cast<bf16x4*>(&L.dst[1][row * DSTR + col + 4]) = bf16x4{};
   }
   lstore(0);
   gload(qt0 + 1 < nqt ? qt0 + 1 : qt0);
   __syncthreads();
 
-  // Every iteration has the same memory-operation sequence (dQ atomics of the
-  // previous tile, LDS store of the next tile, fetch of the one after), so
-  // each wait covers exactly the fetch issued one iteration earlier. Tile
-  // indices past the end are clamped: that extra work lands in buffers no
-  // later step reads, or adds zeros.
+  // Each iteration ends with the LDS store of the next tile (whose wait
+  // covers the fetch issued one iteration earlier, nothing later), the dQ
+  // step of the previous tile (none before the first) and the fetch of the
+  // tile after next. Tile indices past the end are clamped: that extra work
+  // lands in buffers no later step reads, or adds zeros.
   const int qdiag = qt0 + BKN / BQ < nqt ? qt0 + BKN / BQ : nqt;
   int qt = qt0;
   for (; qt < qdiag; ++qt) {
@@ -345,8 +342,8 @@ __device__ __forceinline__ void bwd_body(
     } else {
       zero_dst(buf);
     }
-    dq_tile(qt > qt0 ? qt - 1 : qt0, buf ^ 1);
     lstore(buf ^ 1);
+    if (qt > qt0) dq_tile(qt - 1, buf ^ 1);
     gload(qt + 2 < nqt ? qt + 2 : nqt - 1);
     __syncthreads();
   }
