@@ -350,7 +350,9 @@ int32_t launch_groups(const algx_gemm_batch* groups, int ngroups, bool a_kc, boo
     BatchGemm p;
     if (int32_t rc = fill_batch(groups[i], a_kc, b_kc, symmetric, alpha, beta, p)) return rc;
     if (p.batch == 0 || p.M == 0 || p.N == 0) continue;
-    if (p.K % BK == 0)
+    // (the kernel's A is the caller's B and vice versa)
+    if (p.K % BK == 0 && dma_span_ok(Operand{nullptr, p.ldb, p.N, p.K}, b_kc) &&
+        dma_span_ok(Operand{nullptr, p.lda, p.M, p.K}, a_kc))
       dma[nd++] = p;
     else
       reg[nr++] = p;
@@ -411,7 +413,8 @@ extern "C" int32_t algx_gemm_bf16_splitk(const void* A, const void* B, void* C, 
   hipStream_t s = (hipStream_t)stream;
   const SplitK p{(const bf16*)A, (const bf16*)B, (float*)workspace, lda, ldb, M, N, Kc, splits,
                  tiles_n};
-  const bool dma = Kc % BK == 0;
+  const bool dma = Kc % BK == 0 && dma_span_ok(Operand{nullptr, lda, M, Kc}, a_kc != 0) &&
+                   dma_span_ok(Operand{nullptr, ldb, N, Kc}, b_kc != 0);
   SplitFn fn = dma ? pick_splitk_as<true>(a_kc != 0, b_kc != 0)
                    : pick_splitk_as<false>(a_kc != 0, b_kc != 0);
   hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(kThreads), 0, s, p);

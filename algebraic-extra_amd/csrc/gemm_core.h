@@ -249,6 +249,28 @@ __device__ __forceinline__ int64_t kstep(const Operand& op) {
   return (int64_t)BK * op.ld;                    // the next 32 rows
 }
 
+// Bytes from op.p to the end of the last 16-byte piece the direct-to-LDS
+// loads of a (KC or [k][mn]-stored) operand can read (k stages of BK up to
+// op.K, mn up to op.rows), and whether that fits the loads' 32-bit offsets
+// (with their 1024-byte bias and room to spare). Operands beyond it take the
+// register-staged stages.
+__host__ __device__ inline int64_t dma_span_bytes(const Operand& op, bool kc) {
+  const int64_t stages = (op.K + BK - 1) / BK;
+  int64_t last;  // element offset of the last element read
+  if (kc) {
+    const int64_t step = op.bstride ? op.bstride : BK;
+    last = (stages - 1) * step + (int64_t)(op.rows - 1) * op.ld + (BK - 1);
+  } else {
+    const int64_t col = op.rows - 1 + 7;  // a piece may run to 7 past the last column
+    const int64_t at = op.bstride ? (col >> 5) * op.bstride + (col & 31) : col;
+    last = (stages * BK - 1) * op.ld + at;
+  }
+  return (last + 8) * (int64_t)sizeof(bf16);
+}
+__host__ __device__ inline bool dma_span_ok(const Operand& op, bool kc) {
+  return op.rows > 0 && op.K > 0 && dma_span_bytes(op, kc) <= (int64_t(1) << 32) - 4096;
+}
+
 // MFMA operand (as `operand`) from a swizzled DMA stage.
 template <bool KC>
 __device__ __forceinline__ bf16x8 operand_dma(const bf16* tile, int mn0, int k0, int lane) {
@@ -266,30 +288,36 @@ __device__ __forceinline__ bf16x8 operand_dma(const bf16* tile, int mn0, int k0,
   }
 }
 
-// One LDS-DMA load of a wave: lane i's 16 bytes at src go to dst + 16 i (dst
-// wave-uniform). Issued as inline assembly so that the compiler does not
-// track it: its waitcnt pass cannot tell which LDS buffer such a load writes
-// and would wait for all of them before every LDS read; the ring below waits
-// for its own loads explicitly (wait_vm) before the barrier that publishes
-// them. The assembly sets M0 itself and names it as clobbered; the compiler
-// treats M0 as reserved and uses it nowhere in these kernels (no indirect
-// register indexing, GWS or compiler-issued LDS DMA: every M0 write in their
-// generated code is one of these loads), so no value of its own lives in M0
-// across the statement.
-__device__ __forceinline__ void dma16(const bf16* src, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
+// One LDS-DMA load of a wave: lane i's 16 bytes at sbase + voff (a uniform
+// 64-bit base in SGPRs plus the lane's 32-bit byte offset, the instruction's
+// scalar-base form) go to lds + 16 i (lds wave-uniform). The scalar-base
+// form hands the address unit one 32-bit offset per lane instead of a 64-bit
+// address, which a standalone copy of the k loop measured 1-5 % faster.
+// Issued as inline assembly so that the compiler does not track it: its
+// waitcnt pass cannot tell which LDS buffer such a load writes and would wait
+// for all of them before every LDS read; the ring below waits for its own
+// loads explicitly (wait_vm) before the barrier that publishes them. The
+// assembly sets M0 itself and names it as clobbered; the compiler treats M0
+// as reserved and uses it nowhere in these kernels (no indirect register
+// indexing, GWS or compiler-issued LDS DMA: every M0 write in their generated
+// code is one of these loads), so no value of its own lives in M0 across the
+// statement.
+__device__ __forceinline__ void dma16s(const void* sbase, unsigned voff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff),
+               "s"(sbase)
                : "memory", "m0");
 }
 
-// Two LDS-DMA loads of a wave under one M0: the first block's 16-byte lanes
-// go to lds + 16 i, the second's to lds + 1024 + 16 i through the
-// instruction offset, which the global address takes too (so src1m is the
-// second block's source minus 1024 bytes).
-__device__ __forceinline__ void dma16x2(const bf16* src0, const bf16* src1m, unsigned lds) {
+// Two such loads under one M0: the first block's 16-byte lanes go to
+// lds + 16 i, the second's to lds + 1024 + 16 i through the instruction
+// offset, which the global address takes too (so voff1m is the second
+// block's byte offset minus 1024).
+__device__ __forceinline__ void dma16x2s(const void* sbase, unsigned voff0, unsigned voff1m,
+                                         unsigned lds) {
   asm volatile(
-      "s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
-      "global_load_lds_dwordx4 %2, off offset:1024" ::"s"(lds),
-      "v"(src0), "v"(src1m)
+      "s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %3\n\t"
+      "global_load_lds_dwordx4 %2, %3 offset:1024" ::"s"(lds),
+      "v"(voff0), "v"(voff1m), "s"(sbase)
       : "memory", "m0");
 }
 
@@ -310,9 +338,10 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 
 // Products of a sequence of `ntiles` output tiles with nk k stages each:
 // src(t, a0, a1, b0, b1) gives the wave's four LDS-DMA sources of tile t at
-// k = 0 (dma_src of its A and B blocks 2w and 2w + 1; the operands' k steps
-// stepA / stepB are the same for every tile), epi(t, acc) receives each
-// finished tile. The ring streams across the tiles, so a tile's first stages
+// k = 0 (dma_src of its A and B blocks 2w and 2w + 1, inside the operands
+// that start at baseA / baseB, each spanning less than 4 GiB - 2 KiB; the
+// operands' k steps stepA / stepB are the same for every tile), epi(t, acc)
+// receives each finished tile. The ring streams across the tiles, so a tile's first stages
 // load during the previous tile's last stages and epilogue. Several tiles
 // need nk to be a multiple of the ring's stage count (every tile starts at
 // slot 0).
@@ -326,34 +355,48 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 // same slot, or the stage being read into the slot just consumed, which
 // nothing reads again. Kernels whose epilogue stores a whole output tile pass
 // STORE_HEAVY: such a repeated load would queue behind those stores and hold
-// up the next wait, so they skip it with a branch instead. A pair's second
-// source is passed 1024 bytes low (src - 512 elements): the instruction
-// offset adds the 1024 bytes back to the global address as it does to the
-// LDS one, so a clamped source (dma_src's op.p) still reads in bounds.
+// up the next wait, so they skip it with a branch instead. The loads take
+// the scalar-base form: the lane's source as a 32-bit byte offset from the
+// operand base, biased by 1024 (with the scalar base 1024 bytes low), so that
+// a pair's second block, whose offset is passed 1024 bytes low for the
+// instruction offset to add back, stays non-negative even for a source
+// clamped to the base itself (dma_src's op.p).
 template <bool AKC, bool BKC, bool STORE_HEAVY = false, typename Src, typename Epi>
-__device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t stepB, int ntiles,
+__device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t stepB,
+                                                const bf16* baseA, const bf16* baseB, int ntiles,
                                                 Src&& src, const DmaRing& ring, Acc& acc,
                                                 int tid, Epi&& epi) {
   constexpr int S = kDmaStages, L = S - 2;  // stages in flight beyond the one being read
   const int w = tid >> 6, lane = tid & 63;
   const int wm = w / NWN, wn = w % NWN;
   const int G = ntiles * nk;  // stages of the whole sequence
-  const bf16 *sa0, *sa1, *sb0, *sb1;  // sources of the tile being issued
-  src(0, sa0, sa1, sb0, sb1);
+  // The lane's biased byte offsets of a source pair from its operand base,
+  // and the scalar base of stage kk (1024 bytes below the stage's start).
+  auto boff = [](const bf16* q, const bf16* base) { return (unsigned)((q - base) * 2) + 1024u; };
+  auto sbase = [](const bf16* base, int64_t koff) {
+    return reinterpret_cast<const void*>(reinterpret_cast<uintptr_t>(base + koff) - 1024u);
+  };
+  unsigned oa0, oa1, ob0, ob1;  // sources of the tile being issued
+  {
+    const bf16 *a0, *a1, *b0, *b1;
+    src(0, a0, a1, b0, b1);
+    oa0 = boff(a0, baseA), oa1 = boff(a1, baseA), ob0 = boff(b0, baseB), ob1 = boff(b1, baseB);
+  }
   // Byte offset of the wave's two 1 KB blocks in an operand stage (uniform).
   const unsigned wofs = 2048u * __builtin_amdgcn_readfirstlane(w);
   // The wave's two 1 KB blocks of each operand of stage kk -> slot.
-  auto issue = [&](const bf16* a0, const bf16* a1, const bf16* b0, const bf16* b1, int kk,
-                   bf16* slot) {
+  auto issue = [&](unsigned a0, unsigned a1, unsigned b0, unsigned b1, int kk, bf16* slot) {
     const unsigned dA = lds_addr(slot) + wofs, dB = dA + 2 * kDmaOpElems;
     // Stage offsets as scalars computed here (the compiler would otherwise
     // keep one vector induction variable per unrolled stage).
-    int64_t oa = kk * stepA, ob = kk * stepB;
-    asm volatile("" : "+s"(oa), "+s"(ob));
-    dma16(a0 + oa, dA);
-    dma16(a1 + oa, dA + 1024);
-    dma16(b0 + ob, dB);
-    dma16(b1 + ob, dB + 1024);
+    int64_t ka = kk * stepA, kb = kk * stepB;
+    asm volatile("" : "+s"(ka), "+s"(kb));
+    const void* sA = sbase(baseA, ka);
+    const void* sB = sbase(baseB, kb);
+    dma16s(sA, a0, dA);
+    dma16s(sA, a1, dA + 1024);
+    dma16s(sB, b0, dB);
+    dma16s(sB, b1, dB + 1024);
   };
   // Wait until at most `later` of this wave's stages are still loading (four
   // loads a stage; the loads complete in issue order, and any later vector
@@ -391,7 +434,7 @@ __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t s
   // so every stage is issued two stages before its operands are read.
 #pragma unroll
   for (int u = 0; u < S - 1; ++u)
-    if (u < nk) issue(sa0, sa1, sb0, sb1, u, ring.slot[u]);
+    if (u < nk) issue(oa0, oa1, ob0, ob1, u, ring.slot[u]);
   wait_stages(min(S - 2, G - 1));
   __syncthreads();
   // Register double buffer over half stages: the operands of the next half
@@ -404,8 +447,12 @@ __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t s
   rd(ring.slot[0], 0, xa, xb);
   for (int t = 0; t < ntiles; ++t) {
     // Sources of the next tile, for the stages issued near this tile's end.
-    const bf16 *na0 = sa0, *na1 = sa1, *nb0 = sb0, *nb1 = sb1;
-    if (t + 1 < ntiles) src(t + 1, na0, na1, nb0, nb1);
+    unsigned na0 = oa0, na1 = oa1, nb0 = ob0, nb1 = ob1;
+    if (t + 1 < ntiles) {
+      const bf16 *a0, *a1, *b0, *b1;
+      src(t + 1, a0, a1, b0, b1);
+      na0 = boff(a0, baseA), na1 = boff(a1, baseA), nb0 = boff(b0, baseB), nb1 = boff(b1, baseB);
+    }
     const int g0 = t * nk;
     // `synced`: this stage's wait, barrier and refill already ran before the
     // previous tile's epilogue (the first stage of every tile but the first);
@@ -428,22 +475,22 @@ __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t s
       // (past the end) a repeat of stage kk into the slot just consumed.
       const bool here = kk + S - 1 < nk, next = !here && t + 1 < ntiles;
       const bool fill = !STORE_HEAVY || (!synced && (here || next));
-      const bf16* p0 = next ? na0 : sa0;
-      const bf16* p1 = next ? na1 : sa1;
-      const bf16* q0 = next ? nb0 : sb0;
-      const bf16* q1 = next ? nb1 : sb1;
+      const unsigned p0 = next ? na0 : oa0, p1 = next ? na1 : oa1;
+      const unsigned q0 = next ? nb0 : ob0, q1 = next ? nb1 : ob1;
       const int ks = here ? kk + S - 1 : next ? kk + S - 1 - nk : kk;
       const unsigned dA = lds_addr(refill) + wofs, dB = dA + 2 * kDmaOpElems;
-      int64_t oa = ks * stepA, ob = ks * stepB;
-      asm volatile("" : "+s"(oa), "+s"(ob));
+      int64_t ka = ks * stepA, kb = ks * stepB;
+      asm volatile("" : "+s"(ka), "+s"(kb));
+      const void* sA = sbase(baseA, ka);
+      const void* sB = sbase(baseB, kb);
 #pragma unroll
       for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
           acc.v[i][j] = mfma32(ya[i], yb[j], acc.v[i][j]);
           if (j == TJ - 1 && fill) {
-            if (i == 1) dma16x2(p0 + oa, p1 + (oa - 512), dA);
-            if (i == 3) dma16x2(q0 + ob, q1 + (ob - 512), dB);
+            if (i == 1) dma16x2s(sA, p0, p1 - 1024u, dA);
+            if (i == 3) dma16x2s(sB, q0, q1 - 1024u, dB);
           }
         }
     };
@@ -477,10 +524,10 @@ __device__ __forceinline__ void gemm_stream_dma(int nk, int64_t stepA, int64_t s
     }
     epi(t, acc);
     acc.zero();
-    sa0 = na0;
-    sa1 = na1;
-    sb0 = nb0;
-    sb1 = nb1;
+    oa0 = na0;
+    oa1 = na1;
+    ob0 = nb0;
+    ob1 = nb1;
   }
 }
 
@@ -494,7 +541,7 @@ __device__ __forceinline__ void gemm_seq_dma(const Operand& A, const Operand& B,
   const bf16* b0 = dma_src<BKC>(B, n0, 2 * w, lane);
   const bf16* b1 = dma_src<BKC>(B, n0, 2 * w + 1, lane);
   gemm_stream_dma<AKC, BKC, STORE_HEAVY>(
-      A.K / BK, kstep<AKC>(A), kstep<BKC>(B), ntiles,
+      A.K / BK, kstep<AKC>(A), kstep<BKC>(B), A.p, B.p, ntiles,
       [&](int t, const bf16*& a0, const bf16*& a1, const bf16*& sb0, const bf16*& sb1) {
         a0 = dma_src<AKC>(A, m0 + t * BM, 2 * w, lane);
         a1 = dma_src<AKC>(A, m0 + t * BM, 2 * w + 1, lane);

@@ -435,12 +435,18 @@ template <bool DMA, bool BLK> HeadDzFn pick_head_dz_as(int kind, int log2n) {
     default: return head_dz_kernel<ALGX_HEAD_ALG_CE, 0, DMA, BLK>;
   }
 }
-HeadFwdFn pick_head_fwd(int kind, int log2n, int d) {
-  return d % (BK * kDmaStages) == 0 ? pick_head_fwd_as<true>(kind, log2n)
-                                    : pick_head_fwd_as<false>(kind, log2n);
+// The logit products run direct-to-LDS when d is a whole number of ring
+// turns and E and the token rows fit the loads' 32-bit offsets.
+bool logits_dma(int d, int V, int ntok) {
+  return d % (BK * kDmaStages) == 0 && dma_span_ok(Operand{nullptr, d, V, d}, true) &&
+         dma_span_ok(Operand{nullptr, d, ntok, d}, true);
 }
-HeadDzFn pick_head_dz(int kind, int log2n, int d, bool blocked) {
-  const bool dma = d % (BK * kDmaStages) == 0;
+HeadFwdFn pick_head_fwd(int kind, int log2n, int d, int V, int N) {
+  return logits_dma(d, V, N) ? pick_head_fwd_as<true>(kind, log2n)
+                             : pick_head_fwd_as<false>(kind, log2n);
+}
+HeadDzFn pick_head_dz(int kind, int log2n, int d, bool blocked, int V, int ntok) {
+  const bool dma = logits_dma(d, V, ntok);
   if (blocked)
     return dma ? pick_head_dz_as<true, true>(kind, log2n) : pick_head_dz_as<false, true>(kind, log2n);
   return dma ? pick_head_dz_as<true, false>(kind, log2n) : pick_head_dz_as<false, false>(kind, log2n);
@@ -492,7 +498,7 @@ extern "C" int32_t algx_head_fwd(const void* h, const void* E, const int32_t* ta
                         kind, log2n, inv_c, clamp, s);
   {
     const Probe probe = probe_for(ALGX_PROBE_HEAD_FWD);
-    launch_k(probe, pick_head_fwd(kind, log2n, d),
+    launch_k(probe, pick_head_fwd(kind, log2n, d, V, N),
              grid, dim3(kThreads), s, (const bf16*)h, (const bf16*)E, targets, zt, partial, N, d,
              V, log2n, inv_c, clamp, chunk_tiles_of(N, V));
   }
@@ -540,11 +546,16 @@ extern "C" int32_t algx_head_bwd(const void* h, const void* E, const int32_t* ta
     // stored in 32-column blocks ([v / 32][t][32]): dh's 32-wide k stage
     // reads one 64-byte piece per token row, dE's reads 32 token rows of one
     // block contiguously (2 KB), instead of half lines of 100 KB rows.
-    const bool dma = V % BK == 0 && ntok % BK == 0;
-    const int64_t bstride = dma ? (int64_t)32 * ntok : 0;
+    const int64_t blk = (int64_t)32 * ntok;
+    const bool dma = V % BK == 0 && ntok % BK == 0 &&
+                     dma_span_ok(Operand{nullptr, 32, ntok, V, blk}, true) &&
+                     dma_span_ok(Operand{nullptr, 32, V, ntok, blk}, false) &&
+                     dma_span_ok(Operand{nullptr, d, d, V}, false) &&
+                     dma_span_ok(Operand{nullptr, d, d, ntok}, false);
+    const int64_t bstride = dma ? blk : 0;
     dim3 gdz((ntok + BN - 1) / BN, ((V + BM - 1) / BM + ct - 1) / ct);
     launch_k(probe_for(ALGX_PROBE_HEAD_DZ),
-             pick_head_dz(kind, log2n, d, bstride != 0),
+             pick_head_dz(kind, log2n, d, bstride != 0, V, ntok),
              gdz, dim3(kThreads), s, hb, eb, targets, stat, scale, dz, ldz, bstride, tok0, ntok, d,
              V, log2n, inv_c, clamp, ct);
     if (int32_t rc = check_launch("head_dz")) return rc;
