@@ -87,29 +87,14 @@ __device__ __forceinline__ void fwd_body(
     for (int ks = 0; ks < 4; ++ks)
       qreg[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks);
   }
-  // The guard's k and v rows (reduced below) are fetched now too, so q, these
-  // rows and the K/V prologue tiles share one memory round trip.
-  bf16x8 kxs[4], vxs[4];
-  if (prep.q_s != nullptr && prep.partial != nullptr) {
-    const int64_t krow = base + (int64_t)(q0 + (tid >> 1)) * HD + 32 * (tid & 1);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      kxs[c] = *reinterpret_cast<const bf16x8*>(k + krow + 8 * c);
-      vxs[c] = *reinterpret_cast<const bf16x8*>(v + krow + 8 * c);
-    }
-  }
-  // The pre-scale's q_s and the guard's partial maxima are stored after the
-  // K/V prologue: a store issued before it would make its vmcnt wait also
-  // wait for the store to land.
-  float part_out = 0.0f;
+  // The pre-scale's q_s is stored after the K/V prologue: a store issued
+  // before it would make its vmcnt wait also wait for the store to land.
+  auto nan_to_inf = [](float x) { return x != x ? __builtin_inff() : x; };
+  float sq = 0.0f;  // |q_s|^2 of the lane's row (the guard's partial, below)
   if (prep.q_s != nullptr) {
     // Fused pre-scale: `q` is the raw query; q_s = cast(q * scale)
     // (flash.py:833) is formed in registers and written once for the
-    // backward. With a partial buffer the workgroup also reduces the range
-    // guard's maxima (flash.py:841-849): |q_s|^2 over its 128 query rows and
-    // |k|^2, |v| over the 128 key rows of its diagonal block, so the grid
-    // covers every row once. NaN becomes +inf so that it fails the guard.
-    float sq = 0.0f;
+    // backward.
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       bf16x8 x = qreg[ks];
@@ -121,38 +106,7 @@ __device__ __forceinline__ void fwd_body(
       }
       qreg[ks] = x;
     }
-    if (prep.partial != nullptr) {
-      auto nan_to_inf = [](float x) { return x != x ? __builtin_inff() : x; };
-      sq = nan_to_inf(sq + __shfl_xor(sq, 32, 64));
-      float sk = 0.0f, mv = 0.0f;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const bf16x8 kx = kxs[c];
-        const bf16x8 vx = vxs[c];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float kf = (float)kx[e];
-          sk = __builtin_fmaf(kf, kf, sk);
-          mv = __builtin_fmaxf(mv, nan_to_inf(__builtin_fabsf((float)vx[e])));
-        }
-      }
-      sk = nan_to_inf(sk + __shfl_xor(sk, 1, 64));
-#pragma unroll
-      for (int m = 1; m < 64; m <<= 1) {
-        sq = __builtin_fmaxf(sq, __shfl_xor(sq, m, 64));
-        sk = __builtin_fmaxf(sk, __shfl_xor(sk, m, 64));
-        mv = __builtin_fmaxf(mv, __shfl_xor(mv, m, 64));
-      }
-      if (lane == 0) {
-        red[0][w] = sq;
-        red[1][w] = sk;
-        red[2][w] = mv;
-      }
-      __syncthreads();
-      if (tid < 3)
-        part_out = __builtin_fmaxf(__builtin_fmaxf(red[tid][0], red[tid][1]),
-                                   __builtin_fmaxf(red[tid][2], red[tid][3]));
-    }
+    sq = nan_to_inf(sq + __shfl_xor(sq, 32, 64));
   }
 
   const bool has_sink = sink != nullptr;
@@ -174,7 +128,6 @@ __device__ __forceinline__ void fwd_body(
       bf16* qsp = prep.q_s + base + (int64_t)qrow * HD + 8 * g;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) *reinterpret_cast<bf16x8*>(qsp + 16 * ks) = qreg[ks];
-      if (prep.partial != nullptr && tid < 3) prep.partial[(int64_t)bid * 3 + tid] = part_out;
     }
   };
   if (EARLY_QS) store_prep();
@@ -329,6 +282,49 @@ __device__ __forceinline__ void fwd_body(
     }
     wait_vmcnt<0>();
     __syncthreads();
+  }
+
+  if (prep.q_s != nullptr && prep.partial != nullptr) {
+    // The range guard's partial maxima (flash.py:841-849): |q_s|^2 over the
+    // workgroup's 128 query rows and |k|^2, |v| over the 128 key rows of its
+    // diagonal block (so the grid covers every row once), the k and v rows
+    // read from the two diagonal tiles still in the LDS ring. Thread t takes
+    // physical chunks 4 (t % 2) .. + 3 of row t / 2, so the thread pair
+    // covers the row whatever the chunk placement. NaN becomes +inf so that
+    // it fails the guard.
+    const int r = tid >> 1, slot = (nfull + (r >> 6)) & 1;
+    const bf16* kp = &Kr[slot][(r & 63) * HD + 32 * (tid & 1)];
+    const bf16* vp = &Vr[slot][(r & 63) * HD + 32 * (tid & 1)];
+    float sk = 0.0f, mv = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16x8 kx = *reinterpret_cast<const bf16x8*>(kp + 8 * c);
+      const bf16x8 vx = *reinterpret_cast<const bf16x8*>(vp + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float kf = (float)kx[e];
+        sk = __builtin_fmaf(kf, kf, sk);
+        mv = __builtin_fmaxf(mv, nan_to_inf(__builtin_fabsf((float)vx[e])));
+      }
+    }
+    sk = nan_to_inf(sk + __shfl_xor(sk, 1, 64));
+    float sqm = sq;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      sqm = __builtin_fmaxf(sqm, __shfl_xor(sqm, m, 64));
+      sk = __builtin_fmaxf(sk, __shfl_xor(sk, m, 64));
+      mv = __builtin_fmaxf(mv, __shfl_xor(mv, m, 64));
+    }
+    if (lane == 0) {
+      red[0][w] = sqm;
+      red[1][w] = sk;
+      red[2][w] = mv;
+    }
+    __syncthreads();
+    if (tid < 3)
+      prep.partial[(int64_t)bid * 3 + tid] =
+          __builtin_fmaxf(__builtin_fmaxf(red[tid][0], red[tid][1]),
+                          __builtin_fmaxf(red[tid][2], red[tid][3]));
   }
 
   const float l_tot = l_row + __shfl_xor(l_row, 32, 64);
