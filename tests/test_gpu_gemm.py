@@ -240,3 +240,39 @@ def test_project_gradients_match_torch():
         err = (dw.float() - want).abs().max().item()
         assert err <= 2 ** -7 * want.abs().max().item(), err
         assert (rdw.float() - want).abs().max().item() <= 2 ** -7 * want.abs().max().item()
+
+def _spread_rows(rows, ld):
+    """rows (R, K) laid out ld elements apart in one flat bf16 buffer."""
+    R, K = rows.shape
+    flat = torch.zeros((R - 1) * ld + K, dtype=torch.bfloat16, device=DEV)
+    for r in range(R):
+        flat[r * ld: r * ld + K] = rows[r]
+    return flat
+
+
+def test_operands_beyond_32bit_lane_offsets_take_the_staged_path():
+    """An A operand whose 8 rows lie 4e8 elements apart spans 5.6 GB, past the
+    32-bit lane offsets of the direct-to-LDS loads: the batched and split-K
+    products take the register-staged stages for it (K = 64 would otherwise
+    take the direct-to-LDS ring) and match the float32 reference. A wrong
+    path choice would wrap the offsets inside the allocation and give wrong
+    values, not a fault."""
+    from algebraic_amd import _lib
+    M, N, K, lda = 8, 256, 64, 400_000_000
+    g = torch.Generator(device=DEV).manual_seed(21)
+    rows = torch.randn((M, K), generator=g, device=DEV).bfloat16()
+    B = torch.randn((N, K), generator=g, device=DEV).bfloat16()
+    big = _spread_rows(rows, lda)
+    want = rows.float() @ B.float().t()
+    C = torch.full((M, N), float("nan"), device=DEV, dtype=torch.bfloat16)
+    _lib.call("algx_gemm_bf16_batched", _lib.ptr(big), _lib.ptr(B), None, _lib.ptr(C), 1, M, N,
+              K, 1, 1, 0, lda, K, 0, N, 0, 0, 0, 0, 1.0, 0.0, _lib.stream())
+    _check(C, want)
+    C2 = torch.full((M, N), float("nan"), device=DEV, dtype=torch.bfloat16)
+    ws = torch.empty((_lib.query("algx_gemm_bf16_splitk_workspace_bytes", M, N, 1) // 4,),
+                     device=DEV)
+    _lib.call("algx_gemm_bf16_splitk", _lib.ptr(big), _lib.ptr(B), _lib.ptr(C2), _lib.ptr(ws), M,
+              N, K, 1, 1, lda, K, N, 1, _lib.stream())
+    _check(C2, want)
+    del big
+    torch.cuda.empty_cache()
