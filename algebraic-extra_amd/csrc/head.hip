@@ -242,23 +242,32 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
   auto emit = [&](auto full_tag, int m0, const Acc& acc) {
     constexpr bool FULL = decltype(full_tag)::value;
     // dz of columns mb0 + 8 q4 + 4 g .. + 3 of token column j
+    // d loss / d z of one logit, y the target indicator (fused_head.py:137-145)
+    auto grad = [&](float z, float y, float st) {
+      if (KIND == ALGX_HEAD_CE)
+        return __builtin_amdgcn_exp2f((z - st) * 1.4426950408889634f) - y;
+      const float x = __builtin_fminf(z * inv_c, clamp);
+      float r;
+      const float p = pow_n<L2N>(rho_fast(x, r) * st, log2n);
+      return (p - y) * r;
+    };
     auto run = [&](int mb0, int i, int j, int q4, int tgt, float st) {
       bf16x4 out;
+      const int mr = mb0 + 8 * q4 + 4 * g;  // the run's first column
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int m = mb0 + 8 * q4 + 4 * g + u;
-        const float z = acc.v[i][j][4 * q4 + u];
-        const float y = m == tgt ? 1.0f : 0.0f;
-        float g_z;
-        if (KIND == ALGX_HEAD_CE) {
-          g_z = __builtin_amdgcn_exp2f((z - st) * 1.4426950408889634f) - y;
-        } else {
-          const float x = __builtin_fminf(z * inv_c, clamp);
-          float r;
-          const float p = pow_n<L2N>(rho_fast(x, r) * st, log2n);
-          g_z = (p - y) * r;
-        }
-        out[u] = (bf16)((FULL || m < V) ? g_z * sc : 0.0f);
+      for (int u = 0; u < 4; ++u)
+        out[u] = (bf16)((FULL || mr + u < V) ? grad(acc.v[i][j][4 * q4 + u], 0.0f, st) * sc : 0.0f);
+      // The target (at most one column of the run, rarely any) is formed
+      // again with y = 1, so the common path carries no per-column target test.
+      const unsigned ut = (unsigned)(tgt - mr);
+      if (ut < 4u) {
+        const f32x4 zr = {acc.v[i][j][4 * q4], acc.v[i][j][4 * q4 + 1], acc.v[i][j][4 * q4 + 2],
+                          acc.v[i][j][4 * q4 + 3]};
+        const float zt = ut == 0 ? zr[0] : ut == 1 ? zr[1] : ut == 2 ? zr[2] : zr[3];
+        const bf16 o = (bf16)((FULL || tgt < V) ? grad(zt, 1.0f, st) * sc : 0.0f);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (ut == (unsigned)u) out[u] = o;
       }
       return out;
     };
