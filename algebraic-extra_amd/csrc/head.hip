@@ -251,28 +251,21 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
       const float p = pow_n<L2N>(rho_fast(x, r) * st, log2n);
       return (p - y) * r;
     };
-    auto run = [&](int mb0, int i, int j, int q4, int tgt, float st) {
+    // TGT: some lane of the wave has its token's target among the rows it
+    // holds for this token column, so each logit takes the indicator y; else
+    // y = 0 everywhere ((p - 0) r = p r exactly, so both forms agree bitwise).
+    auto run = [&](auto tgt_tag, int mb0, int i, int j, int q4, int tgt, float st) {
+      constexpr bool TGT = decltype(tgt_tag)::value;
       bf16x4 out;
       const int mr = mb0 + 8 * q4 + 4 * g;  // the run's first column
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        out[u] = (bf16)((FULL || mr + u < V) ? grad(acc.v[i][j][4 * q4 + u], 0.0f, st) * sc : 0.0f);
-      // The target (at most one column of the run, rarely any) is formed
-      // again with y = 1, so the common path carries no per-column target test.
-      const unsigned ut = (unsigned)(tgt - mr);
-      if (ut < 4u) {
-        const f32x4 zr = {acc.v[i][j][4 * q4], acc.v[i][j][4 * q4 + 1], acc.v[i][j][4 * q4 + 2],
-                          acc.v[i][j][4 * q4 + 3]};
-        const float zt = ut == 0 ? zr[0] : ut == 1 ? zr[1] : ut == 2 ? zr[2] : zr[3];
-        const bf16 o = (bf16)((FULL || tgt < V) ? grad(zt, 1.0f, st) * sc : 0.0f);
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (ut == (unsigned)u) out[u] = o;
+      for (int u = 0; u < 4; ++u) {
+        const float y = TGT && mr + u == tgt ? 1.0f : 0.0f;
+        out[u] = (bf16)((FULL || mr + u < V) ? grad(acc.v[i][j][4 * q4 + u], y, st) * sc : 0.0f);
       }
       return out;
     };
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
+    auto column = [&](auto tgt_tag, int j) {
       const int tl = n0 + WTN * wn + 32 * j + c32;  // the same in lanes c32 and c32 + 32
       const int tgt = tgt_j[j];
       const float st = st_j[j];
@@ -288,8 +281,8 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
           bf16* row = dz + (int64_t)(mb0 >> 5) * bstride + (int64_t)tl * 32 + 8 * g;
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            u32x2 d0 = __builtin_bit_cast(u32x2, run(mb0, i, j, 2 * h, tgt, st));
-            u32x2 d1 = __builtin_bit_cast(u32x2, run(mb0, i, j, 2 * h + 1, tgt, st));
+            u32x2 d0 = __builtin_bit_cast(u32x2, run(tgt_tag, mb0, i, j, 2 * h, tgt, st));
+            u32x2 d1 = __builtin_bit_cast(u32x2, run(tgt_tag, mb0, i, j, 2 * h + 1, tgt, st));
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
               // upper half of d0[e] <-> lower half of d1[e]
@@ -303,9 +296,19 @@ __global__ __launch_bounds__(kThreads) void head_dz_kernel(
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4)
             *reinterpret_cast<bf16x4*>(dz + (int64_t)tl * ldz + mb0 + 8 * q4 + 4 * g) =
-                run(mb0, i, j, q4, tgt, st);
+                run(tgt_tag, mb0, i, j, q4, tgt, st);
         }
       }
+    };
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      // A wave's 128 rows hold a target of its 32 tokens in ~8 % of the
+      // (tile, column) pairs at V = 50304; the test is one wave-wide vote.
+      const bool hit = (unsigned)(tgt_j[j] - (m0 + WTM * wm)) < (unsigned)WTM;
+      if (__any(hit))
+        column(std::true_type{}, j);
+      else
+        column(std::false_type{}, j);
     }
   };
   auto emit_tile = [&](int, int m0, const Acc& a) {
