@@ -159,6 +159,33 @@ def test_fused_head_ragged_tiles(N, d, V):
         assert rel_l2(got[3], de) <= 1e-2
 
 
+@pytest.mark.parametrize("kind,n,c", [("alg_ce", 8, 2.0), ("ce", 16, 16.0)])
+def test_fused_head_targets_at_tile_and_wave_edges(kind, n, c):
+    """The forward and dz kernels test for a target once per wave, token
+    column and vocabulary tile (a wave holds 128 rows of a 256-row tile), and
+    handle the target logit only where the test holds. Targets here sit on
+    both sides of every wave and tile edge, inside the last (partial) tile
+    (V = 1000), and 64 consecutive tokens share one target, so whole token
+    columns take the target path while their neighbours do not."""
+    N, d, V = 512, 64, 1000
+    h, e, _ = _head_inputs(N, d, V, 11, 0.2)
+    edges = [0, 1, 126, 127, 128, 129, 254, 255, 256, 257, 383, 384, 511, 512,
+             767, 768, 895, 896, 997, 998, 999]
+    t = np.array([edges[i % len(edges)] for i in range(N)], dtype=np.int64)
+    t[128:192] = 200
+    t = torch.from_numpy(t)
+    got = _head_run(h, e, t, kind=kind, n=n, c=c, block_n=N)
+    (obj, tel), (dh, de) = OH.fused_head(to_np(h), to_np(e), to_np(t), kind=kind, n=n, c=c,
+                                         dtype="bf16", g_obj=1.0)
+    assert abs(got[0] - obj) <= 2e-4 + 2e-3 * abs(obj)
+    np.testing.assert_allclose(got[1], tel, rtol=2e-2, atol=2e-4)
+    assert_bf16(got[2], dh, what="dh")
+    assert rel_l2(got[3], de) <= 1e-2
+    # the target rows of E carry the -y r terms: each checked on its own
+    rows = sorted(set(edges) | {200})
+    assert rel_l2(got[3][rows], de[rows]) <= 1e-2
+
+
 @pytest.mark.parametrize("width", [768, 1024])
 def test_production_head_tiles_at_model_widths(width):
     """test_fused_head_tpu.py:43-67: 256 tokens, V=32768, E ~ 0.02 N(0,1), n=8, c=2."""
